@@ -1,0 +1,360 @@
+/* orc_sampler.c - CPU restatement of the reference token sampler (TEST INFRASTRUCTURE).
+ *
+ * The checker for the GPU sampler: only tests/, the smoke check and the benchmark's CPU
+ * baseline use it.  Semantics follow sample.c (franzvill/quasar); each function cites
+ * the lines it restates.  Build: -O2 -std=c11 -ffp-contract=off (sample.c is built with
+ * -O2 -std=c11, Makefile:9, which under gcc does not contract either).
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "orc_sampler.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+typedef struct { int32_t id; float sc; float p; } orc_cand;
+
+struct orc_sampler {
+    orc_params prm;                 /* clamped parameters (sample.c:47-56) */
+    uint64_t   rng;
+    int32_t   *ring;                /* recent ids; valid slots (head + i) % cap, i < len */
+    int        ring_cap, ring_len, ring_head;
+    float     *work;                /* penalised logits */
+    uint8_t   *mark;                /* history membership, all zero between picks */
+    orc_cand  *cand;
+    int        scratch_n;
+};
+
+#define ORC_DEFAULT_RNG 0x9E3779B97F4A7C15ull
+
+/* sample.c:31-39: greedy defaults, everything disabled. */
+orc_sampler *orc_sampler_new(void) {
+    orc_sampler *s = (orc_sampler *)calloc(1, sizeof *s);
+    if (!s) return NULL;
+    s->prm.temperature = 0.0f;
+    s->prm.top_p = 1.0f;
+    s->prm.top_k = 0;
+    s->prm.min_p = 0.0f;
+    s->prm.repeat_penalty = 1.0f;
+    s->prm.repeat_last_n = 0;
+    s->rng = ORC_DEFAULT_RNG;
+    return s;
+}
+
+/* sample.c:41-45 (NULL-safe). */
+void orc_sampler_free(orc_sampler *s) {
+    if (!s) return;
+    free(s->ring);
+    free(s->work);
+    free(s->mark);
+    free(s->cand);
+    free(s);
+}
+
+/* sample.c:47-68: clamp to the disable values, seed the generator, size the ring only
+ * when its capacity changes, and always empty the history. */
+void orc_sampler_config(orc_sampler *s, float temperature, float top_p, int top_k,
+                        float min_p, float repeat_penalty, int repeat_last_n,
+                        uint64_t seed) {
+    s->prm.temperature = temperature;
+    s->prm.top_p = (top_p > 0.0f && top_p < 1.0f) ? top_p : 1.0f;
+    s->prm.top_k = top_k > 0 ? top_k : 0;
+    s->prm.min_p = min_p > 0.0f ? min_p : 0.0f;
+    s->prm.repeat_penalty = repeat_penalty > 1.0f ? repeat_penalty : 1.0f;
+    s->prm.repeat_last_n = repeat_last_n > 0 ? repeat_last_n : 0;
+    if (seed == 0) seed = (uint64_t)time(NULL) * 2654435761u + 0x1234567u;
+    s->rng = seed ? seed : ORC_DEFAULT_RNG;
+    int cap = s->prm.repeat_last_n;
+    if (cap > 0 && cap != s->ring_cap) {
+        free(s->ring);
+        s->ring = (int32_t *)calloc((size_t)cap, sizeof(int32_t));
+        s->ring_cap = s->ring ? cap : 0;
+    }
+    s->ring_len = 0;
+    s->ring_head = 0;
+}
+
+/* sample.c:70: history only; the generator state is kept. */
+void orc_sampler_reset(orc_sampler *s) { s->ring_len = 0; s->ring_head = 0; }
+
+/* sample.c:72-77: xorshift64 with the xorshift64* output multiplier. */
+uint64_t orc_xorshift64(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return x * 0x2545F4914F6CDD1Dull;
+}
+
+/* sample.c:79-81: top 53 bits scaled to [0, 1). */
+double orc_rng_unit(uint64_t *state) {
+    return (double)(orc_xorshift64(state) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+/* sample.c:83-92: append, or overwrite the oldest once the ring is full. */
+static void orc_record(orc_sampler *s, int id) {
+    if (s->ring_cap <= 0) return;
+    if (s->ring_len < s->ring_cap) {
+        s->ring[(s->ring_head + s->ring_len) % s->ring_cap] = id;
+        s->ring_len++;
+    } else {
+        s->ring[s->ring_head] = id;
+        s->ring_head = (s->ring_head + 1) % s->ring_cap;
+    }
+}
+
+/* sample.c:94-104 (growth of the per-vocabulary scratch). */
+static int orc_scratch(orc_sampler *s, int n) {
+    if (s->scratch_n >= n) return 0;
+    float *w = (float *)realloc(s->work, (size_t)n * sizeof(float));
+    if (w) s->work = w;
+    uint8_t *m = (uint8_t *)realloc(s->mark, (size_t)n);
+    if (m) s->mark = m;
+    orc_cand *c = (orc_cand *)realloc(s->cand, (size_t)n * sizeof(orc_cand));
+    if (c) s->cand = c;
+    if (!w || !m || !c) return -1;
+    memset(s->mark, 0, (size_t)n);
+    s->scratch_n = n;
+    return 0;
+}
+
+/* Order of sample.c:151 under glibc: p descending, ties by ascending id.  When every p
+ * is NaN (degenerate rows) the comparisons are all false and id order remains. */
+static int orc_cmp(const void *a, const void *b) {
+    const orc_cand *x = (const orc_cand *)a, *y = (const orc_cand *)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return (x->id > y->id) - (x->id < y->id);
+}
+
+/* The valid ring slots, oldest first. */
+static int32_t orc_ring_at(const orc_sampler *s, int i) {
+    return s->ring[(s->ring_head + i) % s->ring_cap];
+}
+
+/* sample.c:111-179. */
+int orc_sampler_pick_diag(orc_sampler *s, const float *logits, int n_vocab, orc_diag *dg) {
+    orc_diag scratch_diag;
+    if (!dg) dg = &scratch_diag;
+    memset(dg, 0, sizeof *dg);
+    dg->bdist = INFINITY;
+
+    if (n_vocab <= 0) { dg->rng_after = s->rng; return 0; }           /* :112 */
+    if (orc_scratch(s, n_vocab) != 0) {                                 /* :113-116 */
+        int bi = 0;
+        for (int i = 1; i < n_vocab; i++) if (logits[i] > logits[bi]) bi = i;
+        orc_record(s, bi);
+        dg->id = bi; dg->greedy = 1; dg->rng_after = s->rng;
+        return bi;
+    }
+
+    /* :118-128 penalty (each history id once) and the running max. */
+    const float rp = s->prm.repeat_penalty;
+    const int penalise = rp > 1.0f;
+    if (penalise)
+        for (int i = 0; i < s->ring_len; i++) s->mark[orc_ring_at(s, i)] = 1;
+    float maxl = -INFINITY;
+    for (int i = 0; i < n_vocab; i++) {
+        float l = logits[i];
+        if (s->mark[i]) l = (l > 0.0f) ? l / rp : l * rp;
+        s->work[i] = l;
+        if (l > maxl) maxl = l;
+    }
+    if (penalise)
+        for (int i = 0; i < s->ring_len; i++) s->mark[orc_ring_at(s, i)] = 0;
+    dg->maxl = maxl;
+
+    /* :130-134 greedy: first index of the maximum. */
+    if (s->prm.temperature <= 0.0f) {
+        int bi = 0;
+        for (int i = 1; i < n_vocab; i++) if (s->work[i] > s->work[bi]) bi = i;
+        orc_record(s, bi);
+        dg->id = bi; dg->greedy = 1; dg->rng_after = s->rng;
+        return bi;
+    }
+
+    /* :136-144 the 30-nat window of temperature-scaled logits, ascending ids. */
+    const float inv_t = 1.0f / s->prm.temperature;
+    const float msc = maxl * inv_t;
+    const float thr = msc - 30.0f;
+    int nc = 0;
+    for (int i = 0; i < n_vocab; i++) {
+        float sc = s->work[i] * inv_t;
+        if (sc >= thr) { s->cand[nc].id = i; s->cand[nc].sc = sc; nc++; }
+    }
+    dg->msc = msc;
+    dg->n_window = nc;
+
+    if (nc == 0) {
+        /* Only when thr is NaN (1/T overflows with a zero max, or T is NaN).  sample.c then
+         * returns the id left in its scratch by an earlier call; here that id is 0. */
+        dg->u = orc_rng_unit(&s->rng);
+        orc_record(s, 0);
+        dg->id = 0; dg->keep = 1; dg->rng_after = s->rng;
+        return 0;
+    }
+
+    /* :146-150 softmax numerators in float, denominator accumulated in double. */
+    double sum = 0.0;
+    for (int i = 0; i < nc; i++) {
+        float e = expf(s->cand[i].sc - msc);
+        s->cand[i].p = e;
+        sum += e;
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int i = 0; i < nc; i++) s->cand[i].p = s->cand[i].p * inv;
+    dg->sum = sum;
+    dg->inv = inv;
+
+    /* :151 */
+    qsort(s->cand, (size_t)nc, sizeof(orc_cand), orc_cmp);
+    dg->p0 = s->cand[0].p;
+
+    /* :153-154 top-k */
+    int n = nc;
+    if (s->prm.top_k > 0 && s->prm.top_k < n) n = s->prm.top_k;
+    dg->keep_topk = n;
+    /* :155-160 top-p: shortest prefix whose double running sum reaches top_p. */
+    if (s->prm.top_p < 1.0f) {
+        double cum = 0.0;
+        int keep = n;
+        for (int i = 0; i < n; i++) {
+            cum += s->cand[i].p;
+            if (cum >= s->prm.top_p) { keep = i + 1; break; }
+        }
+        n = keep;
+    }
+    dg->keep_topp = n;
+    /* :161-168 min-p against the top probability. */
+    if (s->prm.min_p > 0.0f) {
+        const float floor_p = s->prm.min_p * s->cand[0].p;
+        int keep = n;
+        for (int i = 1; i < n; i++)
+            if (s->cand[i].p < floor_p) { keep = i; break; }
+        n = keep;
+    }
+    if (n < 1) n = 1;
+    dg->keep = n;
+
+    /* :170-175 draw over the kept prefix. */
+    double rsum = 0.0;
+    for (int i = 0; i < n; i++) rsum += s->cand[i].p;
+    const double u = orc_rng_unit(&s->rng);
+    const double r = u * rsum;
+    double acc = 0.0;
+    int chosen = s->cand[n - 1].id, rank = n - 1;
+    for (int i = 0; i < n; i++) {
+        acc += s->cand[i].p;
+        if (r <= acc) { chosen = s->cand[i].id; rank = i; break; }
+    }
+    dg->rsum = rsum;
+    dg->u = u;
+    dg->rank = rank;
+    /* Distance of u from the nearest CDF boundary of the kept prefix. */
+    {
+        double a = 0.0, best = INFINITY;
+        for (int i = 0; i < n; i++) {
+            a += s->cand[i].p;
+            double d = fabs(u - a / rsum);
+            if (d < best) best = d;
+        }
+        dg->bdist = best;
+    }
+
+    orc_record(s, chosen);                                              /* :177-178 */
+    dg->id = chosen;
+    dg->rng_after = s->rng;
+    return chosen;
+}
+
+int orc_sampler_pick(orc_sampler *s, const float *logits, int n_vocab) {
+    return orc_sampler_pick_diag(s, logits, n_vocab, NULL);
+}
+
+void orc_sampler_set_history(orc_sampler *s, const int32_t *ids, int n) {
+    s->ring_len = 0;
+    s->ring_head = 0;
+    for (int i = 0; i < n; i++) orc_record(s, ids[i]);
+}
+
+int orc_sampler_get_history(const orc_sampler *s, int32_t *out, int cap) {
+    int n = s->ring_len < cap ? s->ring_len : cap;
+    for (int i = 0; i < n; i++) out[i] = orc_ring_at(s, i);
+    return s->ring_len;
+}
+
+uint64_t orc_sampler_get_rng(const orc_sampler *s) { return s->rng; }
+
+void orc_sampler_get_params(const orc_sampler *s, float *f, int32_t *i) {
+    f[0] = s->prm.temperature; f[1] = s->prm.top_p; f[2] = s->prm.min_p;
+    f[3] = s->prm.repeat_penalty;
+    i[0] = s->prm.top_k; i[1] = s->prm.repeat_last_n; i[2] = s->ring_cap;
+}
+void orc_sampler_set_rng(orc_sampler *s, uint64_t rng) { s->rng = rng; }
+
+/* ---- CPU baseline driver ------------------------------------------------------------ */
+
+typedef struct {
+    const orc_params *p;
+    const float *logits;
+    long stride;
+    int r0, r1, n_vocab, hist_n;
+    const int32_t *hist;
+    const uint64_t *seeds;
+    int32_t *out;
+    double secs;
+} orc_job;
+
+static double orc_now(void) {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+static void *orc_job_run(void *arg) {
+    orc_job *j = (orc_job *)arg;
+    orc_sampler *s = orc_sampler_new();
+    j->secs = 0.0;
+    if (!s) return NULL;
+    for (int r = j->r0; r < j->r1; r++) {
+        const orc_params *p = j->p;
+        orc_sampler_config(s, p->temperature, p->top_p, p->top_k, p->min_p, p->repeat_penalty,
+                           p->repeat_last_n, j->seeds[r]);
+        if (j->hist_n > 0) orc_sampler_set_history(s, j->hist + (long)r * j->hist_n, j->hist_n);
+        double t0 = orc_now();
+        j->out[r] = orc_sampler_pick(s, j->logits + (long)r * j->stride, j->n_vocab);
+        j->secs += orc_now() - t0;
+    }
+    orc_sampler_free(s);
+    return NULL;
+}
+
+double orc_pick_rows(const orc_params *p, const float *logits, long row_stride, int n_rows,
+                     int n_vocab, const int32_t *hist, int hist_n, const uint64_t *seeds,
+                     int32_t *out, int n_threads) {
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > n_rows) n_threads = n_rows > 0 ? n_rows : 1;
+    orc_job *jobs = (orc_job *)calloc((size_t)n_threads, sizeof(orc_job));
+    pthread_t *th = (pthread_t *)calloc((size_t)n_threads, sizeof(pthread_t));
+    if (!jobs || !th) { free(jobs); free(th); return -1.0; }
+    for (int t = 0; t < n_threads; t++) {
+        orc_job *j = &jobs[t];
+        j->p = p; j->logits = logits; j->stride = row_stride; j->n_vocab = n_vocab;
+        j->hist = hist; j->hist_n = hist_n; j->seeds = seeds; j->out = out;
+        j->r0 = (int)((long)n_rows * t / n_threads);
+        j->r1 = (int)((long)n_rows * (t + 1) / n_threads);
+    }
+    for (int t = 1; t < n_threads; t++) pthread_create(&th[t], NULL, orc_job_run, &jobs[t]);
+    orc_job_run(&jobs[0]);
+    double worst = jobs[0].secs;
+    for (int t = 1; t < n_threads; t++) {
+        pthread_join(th[t], NULL);
+        if (jobs[t].secs > worst) worst = jobs[t].secs;
+    }
+    free(jobs);
+    free(th);
+    return worst;
+}

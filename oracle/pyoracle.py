@@ -1,0 +1,254 @@
+"""ctypes bindings for the CPU checker libraries (TEST INFRASTRUCTURE ONLY).
+
+Loaded only by tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg,
+always as the checker or the timed CPU baseline, never on the product path.
+
+* ``Oracle``      - oracle/liboracle.so: the C restatement of the reference sampler
+                    (sample.c:31-179), plus host builds of the product's generator and
+                    libm-compatible expf.
+* ``RefSampler``  - oracle/_ref/libref_sample.so: the reference's own sample.c compiled
+                    by oracle/Makefile (present only where that source was available at
+                    build time; it is a built file and travels with the tree).
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libref_sample.so")
+
+
+class Params(C.Structure):
+    """Same layout as orc_params / ref_params."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("top_k", C.c_int32),
+                ("repeat_last_n", C.c_int32)]
+
+
+class Diag(C.Structure):
+    """orc_diag."""
+    _fields_ = [("id", C.c_int32), ("greedy", C.c_int32), ("n_window", C.c_int32),
+                ("keep_topk", C.c_int32), ("keep_topp", C.c_int32), ("keep", C.c_int32),
+                ("rank", C.c_int32), ("pad", C.c_int32),
+                ("maxl", C.c_float), ("msc", C.c_float), ("inv", C.c_float), ("p0", C.c_float),
+                ("sum", C.c_double), ("rsum", C.c_double), ("u", C.c_double),
+                ("bdist", C.c_double), ("rng_after", C.c_uint64)]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_ if f != "pad"}
+
+
+_F = C.POINTER(C.c_float)
+_I = C.POINTER(C.c_int32)
+_U = C.POINTER(C.c_uint64)
+
+
+def _fptr(a):
+    return a.ctypes.data_as(_F)
+
+
+def _iptr(a):
+    return a.ctypes.data_as(_I)
+
+
+def _uptr(a):
+    return a.ctypes.data_as(_U)
+
+
+def _sampler_protos(lib, prefix):
+    vp = C.c_void_p
+    getattr(lib, prefix + "new").restype = vp
+    getattr(lib, prefix + "new").argtypes = []
+    getattr(lib, prefix + "free").argtypes = [vp]
+    getattr(lib, prefix + "config").argtypes = [vp, C.c_float, C.c_float, C.c_int, C.c_float,
+                                               C.c_float, C.c_int, C.c_uint64]
+    getattr(lib, prefix + "reset").argtypes = [vp]
+    getattr(lib, prefix + "pick").argtypes = [vp, _F, C.c_int]
+    getattr(lib, prefix + "pick").restype = C.c_int
+
+
+class _SamplerBase:
+    """Stateful sampler mirroring sample.h (new / config / reset / pick / free)."""
+
+    def __init__(self, lib, prefix, hooks):
+        self._lib, self._p, self._h = lib, prefix, hooks
+        self._s = getattr(lib, prefix + "new")()
+        if not self._s:
+            raise MemoryError("sampler_new returned NULL")
+
+    def close(self):
+        if self._s:
+            getattr(self._lib, self._p + "free")(self._s)
+            self._s = None
+
+    __del__ = close
+
+    def config(self, temperature=0.0, top_p=1.0, top_k=0, min_p=0.0, repeat_penalty=1.0,
+               repeat_last_n=0, seed=1):
+        getattr(self._lib, self._p + "config")(self._s, temperature, top_p, int(top_k), min_p,
+                                               repeat_penalty, int(repeat_last_n),
+                                               int(seed) & 0xFFFFFFFFFFFFFFFF)
+
+    def reset(self):
+        getattr(self._lib, self._p + "reset")(self._s)
+
+    def pick(self, logits):
+        a = np.ascontiguousarray(logits, dtype=np.float32)
+        return getattr(self._lib, self._p + "pick")(self._s, _fptr(a), a.size)
+
+    def set_history(self, ids):
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        getattr(self._lib, self._h + "set_history")(self._s, _iptr(a), a.size)
+
+    def history(self, cap=1 << 16):
+        out = np.zeros(cap, dtype=np.int32)
+        n = getattr(self._lib, self._h + "get_history")(self._s, _iptr(out), cap)
+        return out[:min(n, cap)].copy()
+
+    def params(self):
+        """Stored parameters after the config clamps: (temperature, top_p, min_p,
+        repeat_penalty, top_k, repeat_last_n, ring capacity)."""
+        f = np.zeros(4, dtype=np.float32)
+        i = np.zeros(3, dtype=np.int32)
+        getattr(self._lib, self._h + "get_params")(self._s, _fptr(f), _iptr(i))
+        return tuple(float(x) for x in f) + tuple(int(x) for x in i)
+
+    @property
+    def rng(self):
+        return getattr(self._lib, self._h + "get_rng")(self._s)
+
+    @rng.setter
+    def rng(self, v):
+        getattr(self._lib, self._h + "set_rng")(self._s, int(v) & 0xFFFFFFFFFFFFFFFF)
+
+
+def _hook_protos(lib, h):
+    vp = C.c_void_p
+    getattr(lib, h + "set_history").argtypes = [vp, _I, C.c_int]
+    getattr(lib, h + "get_history").argtypes = [vp, _I, C.c_int]
+    getattr(lib, h + "get_history").restype = C.c_int
+    getattr(lib, h + "get_rng").argtypes = [vp]
+    getattr(lib, h + "get_rng").restype = C.c_uint64
+    getattr(lib, h + "set_rng").argtypes = [vp, C.c_uint64]
+    getattr(lib, h + "get_params").argtypes = [vp, _F, _I]
+
+
+def _rows_protos(fn):
+    fn.argtypes = [C.POINTER(Params), _F, C.c_long, C.c_int, C.c_int, _I, C.c_int, _U, _I,
+                   C.c_int]
+    fn.restype = C.c_double
+
+
+def _pick_rows(fn, params, logits, n_rows, n_vocab, hist, seeds, n_threads):
+    """Shared body of the threaded CPU drivers; returns (ids, seconds)."""
+    logits = np.asarray(logits, dtype=np.float32)
+    assert logits.flags.c_contiguous and logits.ndim == 2 and logits.shape[0] >= n_rows
+    stride = logits.shape[1]
+    seeds = np.ascontiguousarray(seeds, dtype=np.uint64)
+    if hist is None:
+        hist = np.zeros((n_rows, 0), dtype=np.int32)
+    hist = np.ascontiguousarray(hist, dtype=np.int32)
+    out = np.zeros(n_rows, dtype=np.int32)
+    secs = fn(C.byref(params), _fptr(logits), stride, n_rows, n_vocab, _iptr(hist),
+              hist.shape[1] if hist.ndim == 2 else 0, _uptr(seeds), _iptr(out), n_threads)
+    return out, secs
+
+
+class Oracle:
+    """The C restatement (liboracle.so)."""
+
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (run `make -C oracle`)")
+        self.lib = lib = C.CDLL(path)
+        _sampler_protos(lib, "orc_sampler_")
+        _hook_protos(lib, "orc_sampler_")
+        _rows_protos(lib.orc_pick_rows)
+        lib.orc_sampler_pick_diag.argtypes = [C.c_void_p, _F, C.c_int, C.POINTER(Diag)]
+        lib.orc_sampler_pick_diag.restype = C.c_int
+        lib.orc_xorshift64.argtypes = [_U]
+        lib.orc_xorshift64.restype = C.c_uint64
+        lib.orc_rng_unit.argtypes = [_U]
+        lib.orc_rng_unit.restype = C.c_double
+        lib.orc_gen_logits.argtypes = [C.c_int32, C.c_float, C.c_float, C.c_uint64, C.c_long,
+                                       C.c_int, C.c_int, _F, C.c_long]
+        lib.orc_gen_hist.argtypes = [C.c_uint64, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int,
+                                     _I]
+        lib.orc_gen_row_seed.argtypes = [C.c_uint64, C.c_long]
+        lib.orc_gen_row_seed.restype = C.c_uint64
+        lib.orc_product_expf.argtypes = [C.c_float]
+        lib.orc_product_expf.restype = C.c_float
+        lib.orc_check_expf_range.argtypes = [C.c_float, C.c_float, C.c_int]
+        lib.orc_check_expf_range.restype = C.c_long
+
+    def sampler(self):
+        s = _SamplerBase(self.lib, "orc_sampler_", "orc_sampler_")
+        lib = self.lib
+
+        def pick_diag(logits):
+            a = np.ascontiguousarray(logits, dtype=np.float32)
+            d = Diag()
+            lib.orc_sampler_pick_diag(s._s, _fptr(a), a.size, C.byref(d))
+            return d.id, d.as_dict()
+        s.pick_diag = pick_diag
+        return s
+
+    def pick_rows(self, params, logits, n_rows, n_vocab, hist, seeds, n_threads=1):
+        return _pick_rows(self.lib.orc_pick_rows, params, logits, n_rows, n_vocab, hist, seeds,
+                          n_threads)
+
+    def xorshift64(self, state):
+        st = np.array([state], dtype=np.uint64)
+        out = self.lib.orc_xorshift64(_uptr(st))
+        return out, int(st[0])
+
+    def rng_unit(self, state):
+        st = np.array([state], dtype=np.uint64)
+        u = self.lib.orc_rng_unit(_uptr(st))
+        return u, int(st[0])
+
+    def gen_logits(self, dist, sigma, boost, seed, row0, n_rows, n_vocab):
+        out = np.empty((n_rows, n_vocab), dtype=np.float32)
+        self.lib.orc_gen_logits(dist, sigma, boost, seed, row0, n_rows, n_vocab, _fptr(out),
+                                n_vocab)
+        return out
+
+    def gen_hist(self, seed, row0, n_rows, hist_n, n_vocab, pool=0):
+        out = np.empty((n_rows, hist_n), dtype=np.int32)
+        self.lib.orc_gen_hist(seed, row0, n_rows, hist_n, n_vocab, pool, _iptr(out))
+        return out
+
+    def gen_row_seeds(self, seed, row0, n_rows):
+        return np.array([self.lib.orc_gen_row_seed(seed, row0 + r) for r in range(n_rows)],
+                        dtype=np.uint64)
+
+    def product_expf(self, x):
+        return self.lib.orc_product_expf(float(x))
+
+    def check_expf_range(self, lo, hi, n_threads=8):
+        return self.lib.orc_check_expf_range(lo, hi, n_threads)
+
+
+class RefSampler:
+    """The reference's own sample.c built into oracle/_ref (see oracle/Makefile)."""
+
+    def __init__(self, path=REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (needs the reference source)")
+        self.lib = lib = C.CDLL(path)
+        _sampler_protos(lib, "quasar_sampler_")
+        _hook_protos(lib, "ref_")
+        _rows_protos(lib.ref_pick_rows)
+
+    @staticmethod
+    def available(path=REF_SO):
+        return os.path.exists(path)
+
+    def sampler(self):
+        return _SamplerBase(self.lib, "quasar_sampler_", "ref_")
+
+    def pick_rows(self, params, logits, n_rows, n_vocab, hist, seeds, n_threads=1):
+        return _pick_rows(self.lib.ref_pick_rows, params, logits, n_rows, n_vocab, hist, seeds,
+                          n_threads)

@@ -1,0 +1,106 @@
+/* ref_harness.c - builds the reference sampler itself, from its own source, as a checker.
+ *
+ * TEST INFRASTRUCTURE ONLY.  The Makefile compiles this file with REF_SAMPLE_C naming the
+ * reference's sample.c where it lies (its source is never copied into this repository);
+ * the result goes to oracle/_ref/ and is used to generate golden fixtures, to cross-check
+ * the restatement in orc_sampler.c, and as the timed CPU baseline.
+ *
+ * The reference's struct is private to sample.c, so the harness includes that file to
+ * reach it and adds what the five public functions cannot do: preload a history (the
+ * workloads start with one), and read back the generator state and the ring. */
+#define _POSIX_C_SOURCE 200809L
+#include REF_SAMPLE_C
+
+#include <pthread.h>
+
+void ref_set_history(quasar_sampler *s, const int32_t *ids, int n) {
+    s->hist_len = 0;
+    s->hist_head = 0;
+    for (int i = 0; i < n; i++) record(s, ids[i]);
+}
+
+int ref_get_history(const quasar_sampler *s, int32_t *out, int cap) {
+    int n = s->hist_len < cap ? s->hist_len : cap;
+    for (int i = 0; i < n; i++) out[i] = s->hist[(s->hist_head + i) % s->hist_cap];
+    return s->hist_len;
+}
+
+uint64_t ref_get_rng(const quasar_sampler *s) { return s->rng; }
+
+/* The stored (clamped) parameters: f = {temperature, top_p, min_p, repeat_penalty},
+ * i = {top_k, repeat_last_n, hist_cap}. */
+void ref_get_params(const quasar_sampler *s, float *f, int32_t *i) {
+    f[0] = s->temperature; f[1] = s->top_p; f[2] = s->min_p; f[3] = s->repeat_penalty;
+    i[0] = s->top_k; i[1] = s->repeat_last_n; i[2] = s->hist_cap;
+}
+void ref_set_rng(quasar_sampler *s, uint64_t rng) { s->rng = rng; }
+
+typedef struct {
+    float temperature, top_p, min_p, repeat_penalty;
+    int32_t top_k, repeat_last_n;
+} ref_params;
+
+typedef struct {
+    const ref_params *p;
+    const float *logits;
+    long stride;
+    int r0, r1, n_vocab, hist_n;
+    const int32_t *hist;
+    const uint64_t *seeds;
+    int32_t *out;
+    double secs;
+} ref_job;
+
+static double ref_now(void) {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+static void *ref_job_run(void *arg) {
+    ref_job *j = (ref_job *)arg;
+    quasar_sampler *s = quasar_sampler_new();
+    j->secs = 0.0;
+    if (!s) return NULL;
+    for (int r = j->r0; r < j->r1; r++) {
+        const ref_params *p = j->p;
+        quasar_sampler_config(s, p->temperature, p->top_p, p->top_k, p->min_p,
+                              p->repeat_penalty, p->repeat_last_n, j->seeds[r]);
+        if (j->hist_n > 0) ref_set_history(s, j->hist + (long)r * j->hist_n, j->hist_n);
+        double t0 = ref_now();
+        j->out[r] = quasar_sampler_pick(s, j->logits + (long)r * j->stride, j->n_vocab);
+        j->secs += ref_now() - t0;
+    }
+    quasar_sampler_free(s);
+    return NULL;
+}
+
+/* Same contract as orc_pick_rows: one sampler per row, one pick per row, n_threads
+ * POSIX threads over disjoint row ranges; returns the slowest thread's seconds spent
+ * inside quasar_sampler_pick. */
+double ref_pick_rows(const ref_params *p, const float *logits, long row_stride, int n_rows,
+                     int n_vocab, const int32_t *hist, int hist_n, const uint64_t *seeds,
+                     int32_t *out, int n_threads) {
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > n_rows) n_threads = n_rows > 0 ? n_rows : 1;
+    ref_job *jobs = calloc((size_t)n_threads, sizeof(ref_job));
+    pthread_t *th = calloc((size_t)n_threads, sizeof(pthread_t));
+    if (!jobs || !th) { free(jobs); free(th); return -1.0; }
+    for (int t = 0; t < n_threads; t++) {
+        ref_job *j = &jobs[t];
+        j->p = p; j->logits = logits; j->stride = row_stride; j->n_vocab = n_vocab;
+        j->hist = hist; j->hist_n = hist_n; j->seeds = seeds; j->out = out;
+        j->r0 = (int)((long)n_rows * t / n_threads);
+        j->r1 = (int)((long)n_rows * (t + 1) / n_threads);
+    }
+    for (int t = 1; t < n_threads; t++) pthread_create(&th[t], NULL, ref_job_run, &jobs[t]);
+    ref_job_run(&jobs[0]);
+    double worst = jobs[0].secs;
+    for (int t = 1; t < n_threads; t++) {
+        pthread_join(th[t], NULL);
+        if (jobs[t].secs > worst) worst = jobs[t].secs;
+    }
+    free(jobs);
+    free(th);
+    return worst;
+}

@@ -1,0 +1,111 @@
+"""Pins the CPU restatement (oracle/) against the reference's own outputs and against
+closed forms.  CPU only."""
+import math
+import zlib
+
+import numpy as np
+import pytest
+
+from helpers import expect, f32_from_bits, replay, xorshift64_star
+from quasar_amd.workloads import STRESS, WORKLOADS
+
+ALLW = dict(WORKLOADS, **STRESS)
+
+
+def test_clamps_match_reference(oracle, golden):
+    """sample.c:47-68: stored parameters after config, for a grid of inputs."""
+    for c in golden["clamps"]:
+        s = oracle.sampler()
+        s.config(*c["in"], seed=7)
+        assert list(s.params()) == pytest.approx(c["out"], abs=0), c
+
+
+@pytest.mark.parametrize("section", ["edge", "fuzz"])
+def test_small_rows_match_reference(oracle, golden, section):
+    for c in golden[section]:
+        x = f32_from_bits(c["logits_bits"])
+        got = replay(oracle.sampler(), [x], c["params"], int(c["seed"], 16), c["history"],
+                     c["picks"])
+        assert got == expect(c), c["name"]
+
+
+def test_workload_rows_match_reference(oracle, golden):
+    for c in golden["workload"]:
+        w = ALLW[c["workload"]]
+        logits = oracle.gen_logits(w.dist, w.sigma, w.boost, w.seed, c["row"], 1, w.vocab)
+        assert zlib.crc32(logits.tobytes()) == c["logits_crc"], "generator drifted"
+        hist = (oracle.gen_hist(w.seed, c["row"], 1, w.hist_len, w.vocab, w.hist_pool)[0]
+                if w.hist_len else None)
+        if hist is not None:
+            assert zlib.crc32(hist.tobytes()) == c["hist_crc_in"]
+        got = replay(oracle.sampler(), [logits[0]], w.params(), int(c["seed"], 16), hist,
+                     c["picks"])
+        assert got == expect(c), (c["workload"], c["row"])
+
+
+def test_xorshift_closed_form(oracle):
+    """sample.c:72-81 against Python integer arithmetic, including the 2^-53 scaling."""
+    st = 0x9E3779B97F4A7C15
+    for _ in range(1000):
+        out_c, st_c = oracle.xorshift64(st)
+        out_p, st_p = xorshift64_star(st)
+        assert (out_c, st_c) == (out_p, st_p)
+        u, _ = oracle.rng_unit(st)
+        assert u == (out_p >> 11) / 2.0**53 and 0.0 <= u < 1.0
+        st = st_p
+
+
+def test_greedy_is_first_argmax(oracle):
+    """sample.c:130-134: first index of the maximum (numpy argmax agrees on NaN-free rows)."""
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        x = np.round(rng.normal(0, 2, int(rng.integers(1, 300)))).astype(np.float32)
+        s = oracle.sampler()
+        s.config(0.0, 1.0, 0, 0.0, 1.0, 0, 1)
+        assert s.pick(x) == int(np.argmax(x))
+
+
+def test_sampling_invariants(oracle):
+    """Closed-form consequences of sample.c:136-178 on random rows: the chosen id is in
+    the window, top_k=1 takes the head of the (p desc, id asc) order, min_p=1 keeps only
+    ties of the top probability, and a tiny top_p keeps one candidate."""
+    rng = np.random.default_rng(4)
+    for _ in range(100):
+        V = int(rng.integers(2, 400))
+        x = np.round(rng.normal(0, 3, V) * 4).astype(np.float32) / np.float32(4)
+        T = np.float32(rng.choice([0.3, 1.0, 2.0]))
+        s = oracle.sampler()
+        s.config(T, 1.0, 1, 0.0, 1.0, 0, 5)
+        i, d = s.pick_diag(x)
+        inv_t = np.float32(1) / T
+        sc = x * inv_t
+        msc = np.float32(x.max() * inv_t)
+        thr = np.float32(msc - np.float32(30))
+        window = np.nonzero(sc >= thr)[0]
+        assert d["n_window"] == len(window)
+        # head of the order: the largest p; equal p go to the lower id
+        e = np.array([s_ for s_ in sc[window]], dtype=np.float32)
+        e = np.array([math.exp(float(np.float32(v - msc))) for v in e])
+        assert i in window
+        assert x[i] == x.max() or abs(float(sc[i] - msc)) < 1e-6
+        s.config(T, 1.0, 0, 1.0, 1.0, 0, 5)
+        i, d = s.pick_diag(x)
+        assert d["keep"] >= 1 and x[i] * inv_t >= thr
+        s.config(T, 1e-9, 0, 0.0, 1.0, 0, 5)
+        i, d = s.pick_diag(x)
+        assert d["keep"] == 1
+
+
+def test_product_expf_equals_host_libm_on_window(oracle):
+    """The GPU's expf restatement (csrc/qs_expf.h, compiled for the host) equals the host
+    libm expf on every float in [-31, 0] (the softmax window) and on special values."""
+    assert oracle.check_expf_range(-31.0, 0.0, 8) == 0
+    for v in [0.0, -0.0, 1.0, 88.0, 88.7, 89.0, -103.0, -104.0, -200.0, float("inf"),
+              float("-inf")]:
+        a = np.float32(np.exp(np.float64(v))) if abs(v) < 80 else None
+        got = oracle.product_expf(v)
+        if a is not None:
+            assert abs(got - a) <= abs(a) * 2**-23
+    assert math.isnan(oracle.product_expf(float("nan")))
+    assert oracle.product_expf(float("-inf")) == 0.0
+    assert oracle.product_expf(float("inf")) == float("inf")
