@@ -1,0 +1,161 @@
+"""Benchmark: sampled rows/s of the GPU sampler on one MI355X.
+
+A step is one pick over the whole batch of the workload (default: peaked_b256, the
+batch-256 full-sampler workload): repeat penalty, temperature, top-k, softmax, top-p,
+min-p and the seeded draw for every row, logits already resident in HBM.  The timed
+region is `--steps` back-to-back picks between two HIP events on the sampler's stream,
+with a device synchronisation on both sides.  Generator states and histories evolve from
+step to step, as in decoding.
+
+Also reported on the same JSON line:
+  roofline      algorithmic bytes per step (4V logits + 4H history + 4 id + 16 RNG per
+                row) over the measured step time, against 8 TB/s HBM
+  cpu_baseline  the reference's own sample.c (oracle/_ref, when built) or the CPU
+                restatement, on this host's cores, over a bounded sample of the same rows
+  parity        the first step's ids against the CPU on every sampled row
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "sampled rows/s at B=256, V=151936 fp32; achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU work for the baseline sample")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0: all host cores (<= 16)")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(w, logits_host, hist, seeds, gpu_ids, args):
+    """Time the reference sampler (or the restatement) on the host over whole copies of
+    the batch until about args.cpu_seconds of work; check the GPU's first-step ids."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from pyoracle import Oracle, Params, RefSampler
+    if RefSampler.available():
+        impl, kind = RefSampler(), "reference"
+    else:
+        impl, kind = Oracle(), "port"
+    p = Params(*[w.temperature, w.top_p, w.min_p, w.repeat_penalty], w.top_k, w.repeat_last_n)
+    ncores = os.cpu_count() or 1
+    threads = args.cpu_threads or min(ncores, 16)
+    B, V = logits_host.shape
+    total_rows, total_secs, reps = 0, 0.0, 0
+    ids = None
+    while True:
+        ids, secs = impl.pick_rows(p, logits_host, B, V, hist, seeds, threads)
+        total_rows += B
+        total_secs += secs
+        reps += 1
+        if total_secs >= args.cpu_seconds or reps >= 8:
+            break
+    mism = int((ids != gpu_ids).sum())
+    return {"value": total_rows / total_secs, "unit": "rows/s", "cores": threads,
+            "kind": kind,
+            "sample": f"{reps} pass(es) over all {B} rows of {w.name} ({total_rows} picks, "
+                      f"{total_secs:.1f} s of pick time summed over the slowest thread), "
+                      f"{threads} POSIX threads, one sampler per row"}, mism, B
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the sampler's "
+              "rows are independent, so a multi-GPU run is B/G rows per GPU with no "
+              "exchange; run it per GPU.", file=sys.stderr)
+        sys.exit(2)
+    import quasar_amd as qa
+    from quasar_amd.workloads import BENCH_WORKLOAD, STRESS, WORKLOADS
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+    allw = dict(WORKLOADS, **STRESS)
+    w = allw[args.workload or BENCH_WORKLOAD]
+    B, V = w.batch, w.vocab
+    dev_name, dev_mem, dev_cu = qa.device_info()
+    print(f"# device {dev_name}, {dev_mem / 2**30:.0f} GiB, {dev_cu} CUs; workload {w.name}",
+          file=sys.stderr, flush=True)
+
+    logits = qa.DeviceBuffer(4 * B * V)
+    qa.gen_logits_device(logits, V, 0, B, V, w.dist, w.sigma, w.boost, w.seed)
+    from pyoracle import Oracle  # generator helpers only (seeds, history ids)
+    orc = Oracle()
+    seeds = orc.gen_row_seeds(w.seed, 0, B)
+    hist = orc.gen_hist(w.seed, 0, B, w.hist_len, V, w.hist_pool) if w.hist_len else None
+    batch = qa.Batch(B, V, max(1, w.repeat_last_n))
+    batch.config(0, B, *w.params(), seeds=seeds)
+    if hist is not None:
+        batch.set_history(0, hist)
+
+    first_ids, diag = batch.pick(logits.ptr, V, B, V, diag=True)
+    paths = {}
+    for d in diag:
+        paths[d.path] = paths.get(d.path, 0) + 1
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        host = logits.download(np.float32, B * V).reshape(B, V)
+        cpu, mism, checked = cpu_baseline(w, host, hist, seeds, first_ids, args)
+        parity = {"rows_checked": checked, "id_mismatches": mism}
+        del host
+
+    for _ in range(args.warmup):
+        batch.pick_async(logits.ptr, V, B, V)
+    qa.check(qa.load().qs_device_synchronize(), "sync")
+    t0 = time.perf_counter()
+    ms = batch.time_picks(logits.ptr, V, B, V, args.steps)
+    qa.check(qa.load().qs_device_synchronize(), "sync")
+    wall = time.perf_counter() - t0
+
+    ms_per_step = ms / args.steps
+    rows_per_s = B / (ms_per_step * 1e-3)
+    alg_bytes = B * w.algorithmic_bytes_per_row()
+    achieved = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "batch": B, "vocab": V, "history": w.hist_len,
+                   "temperature": w.temperature, "top_k": w.top_k, "top_p": w.top_p,
+                   "min_p": w.min_p, "repeat_penalty": w.repeat_penalty,
+                   "description": w.description},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "one pick (k_scan + k_expsum + k_finalize + k_full)",
+                     "bytes_per_step": alg_bytes},
+        "cpu_baseline": cpu,
+        "parity": parity,
+        "paths": {str(k): v for k, v in sorted(paths.items())},
+        "wall_s_timed": wall,
+        "device": dev_name,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+/* quasar_sampler.h - MI355X (gfx950) token sampler, C ABI.
+ *
+ * Part 1 is the reference's sample.h surface, unchanged: the same five symbols with the
+ * same argument meaning, so the reference's server.o / quasar.o link against this
+ * library instead of sample.o (reference Makefile:17-18 object list).  The work runs on
+ * the GPU; `logits` stays a host pointer, copied in per call.
+ *
+ * Part 2 is the extension the reference does not have: a batch of rows whose logits,
+ * generator states and histories live in device memory, picked in one enqueue.
+ *
+ * Part 3 is plumbing for callers without their own GPU runtime (tests, the benchmark):
+ * device buffers, copies, the synthetic-input generator and event timing.
+ *
+ * Return codes of the extension functions: 0 on success, QS_EINVAL for bad arguments,
+ * QS_ENOMEM when device memory cannot be allocated, QS_EDEVICE for any other HIP
+ * failure; qs_last_error() describes the last failure on the calling thread.
+ */
+#ifndef QUASAR_SAMPLER_H
+#define QUASAR_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------------------
+ * Part 1: sample.h (reference sample.h:12-29)
+ * ------------------------------------------------------------------------------------ */
+
+typedef struct quasar_sampler quasar_sampler;
+
+/* Replaces sample.h:14 (sample.c:31-39).  Defaults: greedy (temperature 0), top_p 1,
+ * top_k 0, min_p 0, repeat_penalty 1, repeat_last_n 0, generator state
+ * 0x9E3779B97F4A7C15.  NULL when host memory is exhausted. */
+quasar_sampler *quasar_sampler_new(void);
+
+/* Replaces sample.h:15 (sample.c:41-45).  NULL-safe. */
+void quasar_sampler_free(quasar_sampler *s);
+
+/* Replaces sample.h:19-22 (sample.c:47-68).  Disable values: top_p outside (0,1) -> 1,
+ * top_k <= 0 -> 0, min_p <= 0 -> 0, repeat_penalty <= 1 -> 1, repeat_last_n <= 0 -> 0.
+ * temperature <= 0 forces greedy.  seed 0 -> time-seeded.  Empties the history. */
+void quasar_sampler_config(quasar_sampler *s, float temperature, float top_p, int top_k,
+                           float min_p, float repeat_penalty, int repeat_last_n,
+                           uint64_t seed);
+
+/* Replaces sample.h:25 (sample.c:70).  Forgets the history; keeps the generator state. */
+void quasar_sampler_reset(quasar_sampler *s);
+
+/* Replaces sample.h:29 (sample.c:111-179).  Picks the next token from the host array
+ * logits[n_vocab] (not modified) and records it in the history.  Returns 0 when
+ * n_vocab <= 0 (no record).  The reference cannot fail past that point; here a device
+ * failure (no GPU, out of device memory) prints one line to stderr and returns -1, since
+ * there is no CPU fallback. */
+int quasar_sampler_pick(quasar_sampler *s, const float *logits, int n_vocab);
+
+/* ------------------------------------------------------------------------------------
+ * Part 2: device-resident batch (extension)
+ * ------------------------------------------------------------------------------------ */
+
+#define QS_EINVAL  (-22)
+#define QS_ENOMEM  (-12)
+#define QS_EDEVICE (-5)
+
+typedef struct qs_batch qs_batch;
+
+/* Per-row report of one pick (optional output of qs_batch_pick). */
+typedef struct {
+    int32_t id;          /* chosen token */
+    int32_t path;        /* QS_PATH_*: how the row was decided */
+    int32_t n_window;    /* ids inside the 30-nat window of the max scaled logit */
+    int32_t n_cand;      /* candidates whose exact probability was computed */
+    int32_t keep_topk;   /* prefix length after top-k */
+    int32_t keep_topp;   /* ... after top-p */
+    int32_t keep;        /* sampled prefix (after min-p, at least 1) */
+    int32_t rank;        /* position of the chosen id in the (p desc, id asc) order */
+    float   maxl;        /* max penalised logit */
+    float   msc;         /* maxl / temperature */
+    float   inv;         /* (float)(1 / sum): the softmax normaliser */
+    float   p0;          /* top probability */
+    double  sum;         /* softmax denominator (double) */
+    double  rsum;        /* mass of the sampled prefix (double) */
+    double  u;           /* uniform draw */
+} qs_pick_diag;
+
+enum {
+    QS_PATH_GREEDY = 0,  /* temperature <= 0: argmax, no draw */
+    QS_PATH_FAST = 1,    /* top candidates preselected by logit, exact order proven */
+    QS_PATH_FULL = 2,    /* whole window sorted on the device (large nucleus, ties across
+                            the preselection boundary, non-finite maxima) */
+    QS_PATH_EMPTY = 3    /* empty window (temperature NaN or 1/T overflowing on a zero
+                            max): id 0, as documented in quasar_sampler_pick */
+};
+
+/* A batch of up to max_rows rows of width up to max_vocab, each with a history ring of
+ * up to max_last_n ids.  Every row starts as quasar_sampler_new() would. */
+qs_batch *qs_batch_new(int max_rows, int max_vocab, int max_last_n);
+void      qs_batch_free(qs_batch *b);
+
+/* quasar_sampler_config applied to rows [row0, row0 + n_rows), row r seeded with
+ * seeds[r - row0] (seeds may be NULL: all rows seeded with 0, i.e. time-seeded).
+ * repeat_last_n above max_last_n is QS_EINVAL. */
+int qs_batch_config(qs_batch *b, int row0, int n_rows, float temperature, float top_p,
+                    int top_k, float min_p, float repeat_penalty, int repeat_last_n,
+                    const uint64_t *seeds);
+
+/* quasar_sampler_reset for rows [row0, row0 + n_rows). */
+int qs_batch_reset(qs_batch *b, int row0, int n_rows);
+
+/* Preload histories: row r receives ids[(r - row0) * n_per_row ...] in order, oldest
+ * first, as if each had been picked (the ring keeps the newest repeat_last_n).  The
+ * workloads start from such histories; sample.h cannot express them. */
+int qs_batch_set_history(qs_batch *b, int row0, int n_rows, const int32_t *ids,
+                         int n_per_row);
+
+/* Pick one token for each of rows [0, n_rows) from device logits d_logits[r*row_stride
+ * + i], i < n_vocab (row_stride >= n_vocab; a 16-byte-aligned base and a stride that is
+ * a multiple of 4 take the vector path).  Writes d_out[r] (device) and, when d_diag is
+ * not NULL, d_diag[r] (device).  Updates each row's generator state and history on the
+ * device.  Asynchronous on the batch's stream. */
+int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
+                  int n_vocab, int32_t *d_out, qs_pick_diag *d_diag);
+
+/* Set one row's generator state and history exactly (oldest first), e.g. to carry a
+ * sampler's state into a larger batch. */
+int qs_batch_set_state(qs_batch *b, int row, uint64_t rng, const int32_t *hist, int n);
+
+/* Wait for everything enqueued on the batch's stream. */
+int qs_batch_synchronize(qs_batch *b);
+
+/* Read one row's generator state and history (oldest first; up to cap ids). */
+int qs_batch_get_state(qs_batch *b, int row, uint64_t *rng, int32_t *hist, int cap,
+                       int *hist_len);
+
+/* The batch's HIP stream (hipStream_t), for callers that order their own work on it. */
+void *qs_batch_stream(qs_batch *b);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char *qs_last_error(void);
+
+/* ------------------------------------------------------------------------------------
+ * Part 3: plumbing for tests and the benchmark
+ * ------------------------------------------------------------------------------------ */
+
+void *qs_device_alloc(size_t bytes);          /* NULL on failure */
+void  qs_device_free(void *p);
+int   qs_memcpy_h2d(void *d_dst, const void *src, size_t bytes);
+int   qs_memcpy_d2h(void *dst, const void *d_src, size_t bytes);
+int   qs_device_synchronize(void);
+/* Name and global memory size of the current device; QS_EDEVICE when there is none. */
+int   qs_device_info(char *name, int name_cap, size_t *total_mem, int *n_cu);
+
+/* Fill rows [row0, row0 + n_rows) of the synthetic workload distribution `dist`
+ * (0 normal, 1 normal plus a boosted column, 2 Student-t with 3 degrees of freedom) into
+ * d_out[(r - row0) * row_stride + i] on the device.  Bit-identical to the host build of
+ * the same generator. */
+int qs_gen_logits_device(float *d_out, int64_t row_stride, int64_t row0, int n_rows,
+                         int n_vocab, int dist, float sigma, float boost, uint64_t seed);
+
+/* y[i] = the library's expf(x[i]) on the device, i < n (the softmax numerator routine,
+ * exposed so tests can compare it with the host C library's expf). */
+int qs_expf_device(const float *d_x, float *d_y, int64_t n);
+
+/* Enqueue `iters` back-to-back qs_batch_pick calls between two HIP events recorded on the
+ * batch's stream, wait, and return the elapsed milliseconds in *ms. */
+int qs_batch_time_picks(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
+                        int n_vocab, int32_t *d_out, int iters, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUASAR_SAMPLER_H */

@@ -37,6 +37,11 @@ uint64_t orc_gen_row_seed(uint64_t seed, long row) { return qs_gen_row_seed(seed
 
 float orc_product_expf(float x) { return qs_expf(x); }
 
+/* The host C library's expf over an array (the reference's softmax numerator routine). */
+void orc_libm_expf_array(const float *x, float *y, long n) {
+    for (long i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
 typedef struct { uint32_t lo, hi; int neg; long bad; } orc_xjob;
 
 /* Walk float bit patterns [lo, hi] of one sign. */

@@ -88,6 +88,8 @@ uint64_t orc_gen_row_seed(uint64_t seed, long row);
 
 /* The product's libm-compatible expf, compiled for the host (checked against expf). */
 float orc_product_expf(float x);
+/* y[i] = host C library expf(x[i]). */
+void  orc_libm_expf_array(const float *x, float *y, long n);
 /* Count x in [lo, hi] (by float ordering, both finite) where the product expf differs
  * from the host expf; n_threads POSIX threads. */
 long  orc_check_expf_range(float lo, float hi, int n_threads);

@@ -180,6 +180,7 @@ class Oracle:
         lib.orc_gen_row_seed.restype = C.c_uint64
         lib.orc_product_expf.argtypes = [C.c_float]
         lib.orc_product_expf.restype = C.c_float
+        lib.orc_libm_expf_array.argtypes = [_F, _F, C.c_long]
         lib.orc_check_expf_range.argtypes = [C.c_float, C.c_float, C.c_int]
         lib.orc_check_expf_range.restype = C.c_long
 
@@ -226,6 +227,12 @@ class Oracle:
 
     def product_expf(self, x):
         return self.lib.orc_product_expf(float(x))
+
+    def libm_expf(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty_like(x)
+        self.lib.orc_libm_expf_array(_fptr(x), _fptr(y), x.size)
+        return y
 
     def check_expf_range(self, lo, hi, n_threads=8):
         return self.lib.orc_check_expf_range(lo, hi, n_threads)

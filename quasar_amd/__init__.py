@@ -1,0 +1,197 @@
+"""quasar_amd - the reference token sampler (sample.c) on MI355X.
+
+Python mirror of the C ABI in include/quasar_sampler.h:
+
+* ``Sampler``  - the reference's five-function API (sample.h:14-29): ``config``,
+                 ``reset``, ``pick`` on host logits, one token per call.
+* ``Batch``    - the device-resident extension: B rows of device logits picked in one
+                 enqueue, generator states and histories kept on the device.
+* ``DeviceBuffer``, ``gen_logits_device`` - plumbing for tests and the benchmark.
+
+Every pick runs the HIP kernels of quasar_amd/csrc/qs_batch.hip; importing the package
+does not load the library, using any of these classes does (and fails loudly if it has
+not been built).
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import _native
+from ._native import (PATH_EMPTY, PATH_FAST, PATH_FULL, PATH_GREEDY, PickDiag, QsError,
+                      check, load)
+
+__all__ = ["Sampler", "Batch", "DeviceBuffer", "gen_logits_device", "device_info",
+           "PickDiag", "QsError", "PATH_GREEDY", "PATH_FAST", "PATH_FULL", "PATH_EMPTY"]
+
+
+class DeviceBuffer:
+    """A device allocation (qs_device_alloc) with numpy upload/download."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = load().qs_device_alloc(self.nbytes)
+        if not self.ptr:
+            raise QsError("qs_device_alloc(%d) failed: %s"
+                          % (self.nbytes, load().qs_last_error().decode()))
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a, offset=0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(load().qs_memcpy_h2d(self.ptr + offset, a.ctypes.data, a.nbytes), "h2d")
+
+    def download(self, dtype, count, offset=0):
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(load().qs_memcpy_d2h(out.ctypes.data, self.ptr + offset, out.nbytes), "d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            load().qs_device_free(self.ptr)
+            self.ptr = None
+
+    __del__ = free
+
+
+def gen_logits_device(buf, row_stride, row0, n_rows, n_vocab, dist, sigma, boost, seed,
+                      offset_rows=0):
+    """Fill rows [row0, row0+n_rows) of a workload distribution into `buf` on the GPU."""
+    check(load().qs_gen_logits_device(buf.ptr + 4 * offset_rows * row_stride, row_stride,
+                                      row0, n_rows, n_vocab, dist, sigma, boost, seed),
+          "qs_gen_logits_device")
+
+
+def device_info():
+    name = C.create_string_buffer(256)
+    mem = C.c_size_t(0)
+    ncu = C.c_int(0)
+    check(load().qs_device_info(name, 256, C.byref(mem), C.byref(ncu)), "qs_device_info")
+    return name.value.decode(), mem.value, ncu.value
+
+
+class Sampler:
+    """sample.h on the GPU: one quasar_sampler (host logits in, one id out)."""
+
+    def __init__(self):
+        self._lib = load()
+        self._s = self._lib.quasar_sampler_new()
+        if not self._s:
+            raise MemoryError("quasar_sampler_new returned NULL")
+
+    def close(self):
+        if getattr(self, "_s", None):
+            self._lib.quasar_sampler_free(self._s)
+            self._s = None
+
+    __del__ = close
+
+    def config(self, temperature=0.0, top_p=1.0, top_k=0, min_p=0.0, repeat_penalty=1.0,
+               repeat_last_n=0, seed=1):
+        self._lib.quasar_sampler_config(self._s, temperature, top_p, int(top_k), min_p,
+                                        repeat_penalty, int(repeat_last_n),
+                                        int(seed) & 0xFFFFFFFFFFFFFFFF)
+
+    def reset(self):
+        self._lib.quasar_sampler_reset(self._s)
+
+    def pick(self, logits):
+        a = np.ascontiguousarray(logits, dtype=np.float32)
+        return self._lib.quasar_sampler_pick(self._s, a.ctypes.data_as(C.POINTER(C.c_float)),
+                                             a.size)
+
+
+class Batch:
+    """qs_batch: rows of device logits picked together, state on the device."""
+
+    def __init__(self, max_rows, max_vocab, max_last_n=0):
+        self._lib = load()
+        self.max_rows, self.max_vocab, self.max_last_n = max_rows, max_vocab, max_last_n
+        self._b = self._lib.qs_batch_new(max_rows, max_vocab, max_last_n)
+        if not self._b:
+            raise QsError("qs_batch_new failed: " + self._lib.qs_last_error().decode())
+        self._out = DeviceBuffer(4 * max_rows)
+        self._diag = DeviceBuffer(C.sizeof(PickDiag) * max_rows)
+
+    def close(self):
+        if getattr(self, "_b", None):
+            self._lib.qs_batch_free(self._b)
+            self._b = None
+
+    __del__ = close
+
+    def config(self, row0, n_rows, temperature=0.0, top_p=1.0, top_k=0, min_p=0.0,
+               repeat_penalty=1.0, repeat_last_n=0, seeds=None):
+        sp = None
+        if seeds is not None:
+            seeds = np.ascontiguousarray(np.asarray(seeds, dtype=np.uint64).reshape(-1))
+            assert seeds.size == n_rows
+            sp = seeds.ctypes.data_as(C.POINTER(C.c_uint64))
+        check(self._lib.qs_batch_config(self._b, row0, n_rows, temperature, top_p, int(top_k),
+                                        min_p, repeat_penalty, int(repeat_last_n), sp),
+              "qs_batch_config")
+
+    def reset(self, row0, n_rows):
+        check(self._lib.qs_batch_reset(self._b, row0, n_rows), "qs_batch_reset")
+
+    def set_history(self, row0, ids):
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+        if ids.ndim == 1:
+            ids = ids.reshape(1, -1)
+        n_rows, n = ids.shape
+        check(self._lib.qs_batch_set_history(self._b, row0, n_rows,
+                                             ids.ctypes.data_as(C.POINTER(C.c_int32)), n),
+              "qs_batch_set_history")
+
+    def set_state(self, row, rng, hist):
+        h = np.ascontiguousarray(np.asarray(hist, dtype=np.int32).reshape(-1))
+        check(self._lib.qs_batch_set_state(self._b, row, int(rng) & 0xFFFFFFFFFFFFFFFF,
+                                           h.ctypes.data_as(C.POINTER(C.c_int32)), h.size),
+              "qs_batch_set_state")
+
+    def get_state(self, row):
+        cap = max(1, self.max_last_n)
+        hist = np.zeros(cap, dtype=np.int32)
+        rng = C.c_uint64(0)
+        n = C.c_int(0)
+        check(self._lib.qs_batch_get_state(self._b, row, C.byref(rng),
+                                           hist.ctypes.data_as(C.POINTER(C.c_int32)), cap,
+                                           C.byref(n)),
+              "qs_batch_get_state")
+        return int(rng.value), hist[:n.value].copy()
+
+    def pick_async(self, logits_ptr, row_stride, n_rows, n_vocab, diag=False):
+        check(self._lib.qs_batch_pick(self._b, logits_ptr, row_stride, n_rows, n_vocab,
+                                      self._out.ptr, self._diag.ptr if diag else None),
+              "qs_batch_pick")
+
+    def pick(self, logits_ptr, row_stride, n_rows, n_vocab, diag=False):
+        """Pick rows [0, n_rows); returns ids (and a list of PickDiag when diag)."""
+        self.pick_async(logits_ptr, row_stride, n_rows, n_vocab, diag)
+        self.synchronize()
+        ids = self._out.download(np.int32, n_rows)
+        if not diag:
+            return ids
+        raw = self._diag.download(np.uint8, C.sizeof(PickDiag) * n_rows)
+        d = (PickDiag * n_rows).from_buffer_copy(raw.tobytes())
+        return ids, list(d)
+
+    def synchronize(self):
+        check(self._lib.qs_batch_synchronize(self._b), "qs_batch_synchronize")
+
+    def time_picks(self, logits_ptr, row_stride, n_rows, n_vocab, iters):
+        ms = C.c_float(0)
+        check(self._lib.qs_batch_time_picks(self._b, logits_ptr, row_stride, n_rows, n_vocab,
+                                            self._out.ptr, iters, C.byref(ms)),
+              "qs_batch_time_picks")
+        return ms.value
+
+    @property
+    def stream(self):
+        return self._lib.qs_batch_stream(self._b)

@@ -1,0 +1,52 @@
+/* qs_params.c - parameter clamps and the error channel (C host code). */
+#define _POSIX_C_SOURCE 200809L
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+
+#include "qs_internal.h"
+
+#define QS_DEFAULT_RNG 0x9E3779B97F4A7C15ull
+
+void qs_default_param(qs_row_param *out, uint64_t *rng_out) {
+    memset(out, 0, sizeof *out);
+    out->temperature = 0.0f;
+    out->top_p = 1.0f;
+    out->top_k = 0;
+    out->min_p = 0.0f;
+    out->repeat_penalty = 1.0f;
+    out->ring_cap = 0;
+    out->inv_t = 0.0f;
+    *rng_out = QS_DEFAULT_RNG;
+}
+
+void qs_clamp_config(float temperature, float top_p, int top_k, float min_p,
+                     float repeat_penalty, int repeat_last_n, uint64_t seed, int prev_cap,
+                     qs_row_param *out, uint64_t *rng_out) {
+    memset(out, 0, sizeof *out);
+    out->temperature = temperature;
+    out->top_p = (top_p > 0.0f && top_p < 1.0f) ? top_p : 1.0f;
+    out->top_k = top_k > 0 ? top_k : 0;
+    out->min_p = min_p > 0.0f ? min_p : 0.0f;
+    out->repeat_penalty = repeat_penalty > 1.0f ? repeat_penalty : 1.0f;
+    out->ring_cap = repeat_last_n > 0 ? repeat_last_n : prev_cap;
+    /* Used whenever the row samples, i.e. unless temperature <= 0 (a NaN temperature
+     * samples, as in sample.c:130); the same float division sample.c:137 does per pick.
+     * volatile keeps it a run-time IEEE division. */
+    volatile float t = temperature;
+    out->inv_t = temperature <= 0.0f ? 0.0f : 1.0f / t;
+    if (seed == 0) seed = (uint64_t)time(NULL) * 2654435761u + 0x1234567u;
+    *rng_out = seed ? seed : QS_DEFAULT_RNG;
+}
+
+static _Thread_local char qs_err[512];
+
+void qs_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(qs_err, sizeof qs_err, fmt, ap);
+    va_end(ap);
+}
+
+const char *qs_last_error(void) { return qs_err; }
