@@ -1,0 +1,542 @@
+// qs_device.h - device code shared by the sampler kernels (included by .hip files only).
+//
+// Conventions: a row is one vector of n_vocab penalised logits; "key" is the
+// order-preserving u32 image of a float (f2key); candidates are kept as keys so any
+// threshold is a plain integer compare.  Every routine here reproduces a step of the
+// reference sampler (sample.c) bit for bit, or is a block-level primitive (select, sort)
+// whose result does not depend on thread scheduling.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstdint>
+
+#include "../../include/quasar_sampler.h"
+#include "qs_expf.h"
+#include "qs_internal.h"
+
+namespace qs {
+
+constexpr int K_MAX = 512;        // largest top-k decided from preselected candidates
+constexpr int K_OFF = 64;         // candidates aimed for when top-k is off
+constexpr int SORT_CAP = 2048;    // candidates the decision step sorts in LDS
+constexpr int SPIN_LIMIT = 1 << 20;  // bounded waits: polls before giving up (~1-2 s)
+
+// ---- keys, lanes, reductions ---------------------------------------------------------------
+
+// Order-preserving map of float bit patterns to unsigned keys (-0 sorts below +0; NaN
+// with the sign bit clear sorts above +inf, so callers filter NaN by float compares).
+__device__ __forceinline__ uint32_t f2key(float f) {
+    uint32_t b = __float_as_uint(f);
+    return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;   // f2key(-inf)
+
+__device__ __forceinline__ int lane_prefix(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+// Butterfly over the wave: every lane ends with the same value and the rounding of the
+// double adds depends only on lane positions, never on timing.
+__device__ __forceinline__ double wave_sum_d(double v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t t = __shfl_xor(v, o, 64);
+        v = t > v ? t : v;
+    }
+    return v;
+}
+__device__ __forceinline__ int wave_or_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+    return v;
+}
+
+// (value desc, index asc) with index < 0 meaning "none": the greedy combine.
+__device__ __forceinline__ void best_combine(float &v, int &i, float ov, int oi) {
+    if (oi >= 0 && (i < 0 || ov > v || (ov == v && oi < i))) { v = ov; i = oi; }
+}
+__device__ __forceinline__ void wave_best(float &v, int &i) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(i, o, 64);
+        best_combine(v, i, ov, oi);
+    }
+}
+
+// ---- the reference's scalar steps ----------------------------------------------------------
+
+// sample.c:124: a history logit is divided by the penalty when positive, multiplied
+// otherwise (so -0, NaN and -inf are unchanged, +inf stays +inf).
+__device__ __forceinline__ float penalise(float l, float rp) {
+    return l > 0.0f ? l / rp : l * rp;
+}
+
+// sample.c:72-81: xorshift64, the xorshift64* output multiplier, top 53 bits.
+__device__ __forceinline__ double rng_unit(uint64_t &st) {
+    uint64_t x = st;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    st = x;
+    return (double)((x * 0x2545F4914F6CDD1Dull) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+// sample.c:83-92: append, or overwrite the oldest once the ring is full.
+__device__ __forceinline__ void ring_record(int32_t *ring, int32_t *hlen, int32_t *hhead,
+                                            int cap, int id) {
+    if (cap <= 0) return;
+    const int len = *hlen, head = *hhead;
+    if (len < cap) {
+        ring[(head + len) % cap] = id;
+        *hlen = len + 1;
+    } else {
+        ring[head] = id;
+        *hhead = (head + 1) % cap;
+    }
+}
+
+__host__ __device__ __forceinline__ bool row_greedy(const qs_row_param &p) {
+    return p.temperature <= 0.0f;      // sample.c:130 (a NaN temperature samples)
+}
+
+// Candidates the decision step aims to keep for a sampling row.  Any value is correct:
+// the decision proves the preselection or hands the row to the full-window path.
+__host__ __device__ __forceinline__ int row_ksel(const qs_row_param &p) {
+    return p.top_k > 0 ? (p.top_k < K_MAX ? p.top_k : K_MAX) : K_OFF;
+}
+
+// ---- per-row device state and scratch ----------------------------------------------------
+
+struct RowState {
+    const qs_row_param *prm;
+    uint64_t *rng;
+    int32_t *ring;
+    int32_t *hlen;
+    int32_t *hhead;
+    int ring_stride;
+};
+
+struct Scratch {
+    float *smax;          // [rows*S] slice max of penalised logits
+    float *bestv;         // [rows*S] greedy: slice max value
+    int32_t *besti;       // [rows*S] greedy: its first index (-1: none)
+    uint32_t *sth;        // [rows*S] slice candidate threshold (key)
+    uint32_t *ckey;       // [rows*S*ccap] candidate keys
+    int32_t *cid;         // [rows*S*ccap] candidate ids
+    int32_t *ccnt;        // [rows*S] candidates per slice
+    uint32_t *crej;       // [rows*S] bound on rejected keys (0: nothing rejected)
+    int32_t *cflag;       // [rows*S] 1: candidate buffer overflowed
+    double *psum;         // [rows*S] double partial softmax denominators
+    int32_t *pcnt;        // [rows*S] window counts
+    int32_t *locks;       // [nslots] full-window scratch slot locks
+    uint64_t *full_keys;  // [nslots][2][vocab]
+    uint32_t *full_bm;    // [nslots][vocab/32+1]
+    int32_t *err;         // [1] sticky error flag (bounded wait gave up)
+    int nslots;
+    int ccap;             // candidates per slice list
+};
+
+struct Geometry {
+    const float *logits;
+    int64_t stride;
+    int vocab;
+    int n_rows;
+    int slices;
+    int slice_len;
+    int bm_words;         // LDS bitmap words per slice
+};
+
+// History membership of [lo, hi) as a bitmap (LDS or global); ids outside are skipped and
+// duplicates set the same bit, so each id is penalised once (sample.c:120).
+template <int NT>
+__device__ void build_bitmap(uint32_t *bm, int words, int lo, int hi, const RowState &st,
+                             int row, int cap) {
+    for (int j = threadIdx.x; j < words; j += NT) bm[j] = 0u;
+    __syncthreads();
+    const int len = st.hlen[row], head = st.hhead[row];
+    const int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+    for (int j = threadIdx.x; j < len; j += NT) {
+        const int id = ring[(head + j) % cap];
+        if (id >= lo && id < hi) atomicOr(&bm[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+    __syncthreads();
+}
+
+// Four consecutive logits starting at element 4c; elements at or past `hi` read as NaN
+// (NaN never raises a max, never passes a filter and never enters the window).
+template <bool VEC>
+__device__ __forceinline__ float4 load4(const float *x, int c, int hi) {
+    const int i = c << 2;
+    if (VEC && i + 3 < hi) return *((const float4 *)x + c);
+    const float q = __builtin_nanf("");
+    float4 v;
+    v.x = i < hi ? x[i] : q;
+    v.y = i + 1 < hi ? x[i + 1] : q;
+    v.z = i + 2 < hi ? x[i + 2] : q;
+    v.w = i + 3 < hi ? x[i + 3] : q;
+    return v;
+}
+
+// ---- block-level select and sort -----------------------------------------------------------
+
+// K-th largest of n keys in LDS (1 <= k <= n), by 8-bit radix select: four rounds of a
+// 256-bin histogram restricted to the prefix found so far.
+template <int NT>
+__device__ uint32_t block_kth(const uint32_t *keys, int n, int k, uint32_t *hist, int *sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    uint32_t prefix = 0u, pmask = 0u;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int j = tid; j < 256; j += NT) hist[j] = 0u;
+        __syncthreads();
+        for (int j = tid; j < n; j += NT) {
+            const uint32_t u = keys[j];
+            if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            uint32_t c[4];
+            for (int q = 0; q < 4; ++q) c[q] = hist[4 * lane + q];
+            const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+            uint32_t incl = mine;                       // sum over lanes >= this one
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_down(incl, o, 64);
+                if (lane + o < 64) incl += t;
+            }
+            const uint32_t excl = incl - mine;
+            if (excl < (uint32_t)k && (uint32_t)k <= incl) {
+                uint32_t run = excl;
+                for (int q = 3; q >= 0; --q) {
+                    if (run + c[q] >= (uint32_t)k) {
+                        sh[0] = 4 * lane + q;
+                        sh[1] = k - (int)run;
+                        break;
+                    }
+                    run += c[q];
+                }
+            }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)sh[0] << shift;
+        pmask |= 255u << shift;
+        k = sh[1];
+        __syncthreads();
+    }
+    return prefix;
+}
+
+// Sort n_pad (a power of two) 64-bit keys in LDS, descending.
+template <int NT>
+__device__ void bitonic_desc(uint64_t *s, int n_pad) {
+    for (int size = 2; size <= n_pad; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < (n_pad >> 1); i += NT) {
+                const int pos = 2 * i - (i & (stride - 1));
+                const int par = pos + stride;
+                const bool desc = (pos & size) == 0;
+                const uint64_t a = s[pos], b = s[par];
+                if ((a < b) == desc) { s[pos] = b; s[par] = a; }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// (p, id) sort key: p's bits above, ~id below, so descending order is p desc, id asc
+// (sample.c:151 under glibc's stable merge sort on ascending ids).
+__device__ __forceinline__ uint64_t pid_key(float p, int id) {
+    return ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)~(uint32_t)id;
+}
+__device__ __forceinline__ float key_p(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)(k & 0xFFFFFFFFull); }
+
+// ---- the decision over sorted candidates (one thread) --------------------------------------
+
+// sample.c:153-178 over the first positions of the (p desc, id asc) order.  srt[0..m)
+// hold in-window candidates; positions [0, E) are known to be positions of the full
+// order.  nwin is the window size.  Returns false (nothing consumed) when the cuts or the
+// draw would read a position >= E; otherwise advances rs and fills id and d.
+__device__ bool decide_prefix(const uint64_t *srt, int E, int nwin, const qs_row_param &P,
+                              uint64_t &rs, int &id, qs_pick_diag &d) {
+    if (E < 1) return false;
+    int n = nwin;                                             // sample.c:153-154
+    if (P.top_k > 0 && P.top_k < n) n = P.top_k;
+    d.keep_topk = n;
+    if (P.top_p < 1.0f) {                                     // sample.c:155-160
+        double cum = 0.0;
+        int keep = n;
+        for (int i = 0; i < n; ++i) {
+            if (i >= E) return false;
+            cum += key_p(srt[i]);
+            if (cum >= P.top_p) { keep = i + 1; break; }
+        }
+        n = keep;
+    }
+    d.keep_topp = n;
+    if (P.min_p > 0.0f) {                                     // sample.c:161-168
+        const float floor_p = P.min_p * key_p(srt[0]);
+        int keep = n;
+        for (int i = 1; i < n; ++i) {
+            if (i >= E) return false;
+            if (key_p(srt[i]) < floor_p) { keep = i; break; }
+        }
+        n = keep;
+    }
+    if (n < 1) n = 1;
+    if (n > E) return false;
+    double rsum = 0.0;                                        // sample.c:170-175
+    for (int i = 0; i < n; ++i) rsum += key_p(srt[i]);
+    const double u = rng_unit(rs);
+    const double r = u * rsum;
+    double acc = 0.0;
+    int rank = n - 1;
+    for (int i = 0; i < n; ++i) {
+        acc += key_p(srt[i]);
+        if (r <= acc) { rank = i; break; }
+    }
+    id = key_id(srt[rank]);
+    d.keep = n;
+    d.rank = rank;
+    d.rsum = rsum;
+    d.u = u;
+    d.p0 = key_p(srt[0]);
+    return true;
+}
+
+// ---- the full-window path ------------------------------------------------------------------
+
+// Stable LSD radix sort of n 64-bit keys, descending, 8 bits per pass; each wavefront
+// owns a contiguous range and ranks equal digits by lane order (ballot multisplit).
+// Returns the buffer holding the result (a or b).  whist: NT/64*256 words, sh: 1 int.
+template <int NT>
+__device__ uint64_t *radix_sort_desc(uint64_t *a, uint64_t *b, int n, uint32_t *whist,
+                                     uint32_t *wsum, int *sh) {
+    constexpr int NWV = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int ch = (n + NWV - 1) / NWV;
+    const int beg = min(wv * ch, n), end = min(beg + ch, n);
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    uint64_t *src = a, *dst = b;
+    for (int shift = 0; shift < 64; shift += 8) {
+        for (int j = tid; j < NWV * 256; j += NT) whist[j] = 0u;
+        if (tid == 0) sh[0] = 0;
+        __syncthreads();
+        for (int base = beg; base < end; base += 64) {
+            const int j = base + lane;
+            if (j < end) atomicAdd(&whist[wv * 256 + 255 - (int)((src[j] >> shift) & 255u)], 1u);
+        }
+        __syncthreads();
+        // exclusive offsets in (digit, wave) order; a pass where one digit holds every
+        // key moves nothing and is skipped.  Threads 0..255 own one digit each.
+        uint32_t tot = 0, incl = 0;
+        if (tid < 256) {
+            for (int w = 0; w < NWV; ++w) tot += whist[w * 256 + tid];
+            if (tot == (uint32_t)n) sh[0] = 1;
+            incl = tot;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            if (lane == 63) wsum[wv] = incl;
+        }
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t run = incl - tot;
+            for (int w = 0; w < wv; ++w) run += wsum[w];
+            for (int w = 0; w < NWV; ++w) {
+                const uint32_t c = whist[w * 256 + tid];
+                whist[w * 256 + tid] = run;
+                run += c;
+            }
+        }
+        __syncthreads();
+        const bool skip = sh[0] != 0;
+        __syncthreads();           // every thread has read sh[0] before the next pass resets it
+        if (skip) continue;
+        for (int base = beg; base < end; base += 64) {
+            const int j = base + lane;
+            const bool valid = j < end;
+            const uint64_t key = valid ? src[j] : 0ull;
+            const int dg = 255 - (int)((key >> shift) & 255u);
+            uint64_t peers = __ballot(valid);
+            for (int bit = 0; bit < 8; ++bit) {
+                const bool on = (dg >> bit) & 1;
+                const uint64_t bb = __ballot(on);
+                peers &= on ? bb : ~bb;
+            }
+            if (valid) {
+                const int rank = __popcll(peers & lt);
+                const uint32_t pos = whist[wv * 256 + dg] + (uint32_t)rank;
+                dst[pos] = key;
+                if ((peers >> lane) == 1ull) whist[wv * 256 + dg] += (uint32_t)__popcll(peers);
+            }
+        }
+        __syncthreads();
+        uint64_t *t = src;
+        src = dst;
+        dst = t;
+    }
+    return src;
+}
+
+// Shared memory a full-window pass needs (static per kernel).
+template <int NT>
+struct FullLds {
+    uint32_t whist[(NT / 64) * 256];
+    uint32_t wsum[NT / 64];
+    int sh[4];
+};
+
+// The whole window of one row, sorted on the device, then sample.c:153-178 sequentially.
+// Takes a scratch slot (bounded wait; on giving up the row gets id -3 and the sticky error
+// flag is set).  maxl/sum/nwin are the row totals of the two streaming passes.
+template <int NT>
+__device__ void full_row(const float *x, int V, int row, const qs_row_param &P, float maxl,
+                         double sum, const RowState &st, const Scratch &sc, int32_t *out,
+                         qs_pick_diag *diag, const uint64_t *tab, FullLds<NT> &fl) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+    if (tid == 0) {
+        int slot = -1;
+        for (int it = 0; it < SPIN_LIMIT; ++it) {
+            const int s = (row + it) % sc.nslots;
+            if (atomicCAS(&sc.locks[s], 0, 1) == 0) { slot = s; break; }
+            if ((it + 1) % sc.nslots == 0) __builtin_amdgcn_s_sleep(16);
+        }
+        fl.sh[0] = slot;
+    }
+    __syncthreads();
+    const int slot = fl.sh[0];
+    __syncthreads();
+    if (slot < 0) {
+        if (tid == 0) {
+            atomicOr(sc.err, 1);
+            out[row] = -3;
+        }
+        return;
+    }
+    uint64_t *ka = sc.full_keys + (int64_t)slot * 2 * V;
+    uint64_t *kb = ka + V;
+    uint32_t *bm = sc.full_bm + (int64_t)slot * (V / 32 + 1);
+
+    const float inv_t = P.inv_t;
+    const float msc = maxl * inv_t;
+    const float thr = msc - 30.0f;
+    const bool deg = !isfinite(msc);       // every p is NaN (sample.c:148 on inf - inf)
+    const float inv = (float)(1.0 / sum);
+    const float rp = P.repeat_penalty;
+    const bool pen = rp > 1.0f && st.hlen[row] > 0 && P.ring_cap > 0;
+    if (pen) build_bitmap<NT>(bm, V / 32 + 1, 0, V, st, row, P.ring_cap);
+    if (tid == 0) fl.sh[1] = 0;
+    __syncthreads();
+    for (int i0 = 0; i0 < V; i0 += NT) {
+        const int i = i0 + tid;
+        bool in = false;
+        uint64_t key = 0ull;
+        if (i < V) {
+            float w = x[i];
+            if (pen && ((bm[i >> 5] >> (i & 31)) & 1u)) w = penalise(w, rp);
+            const float s = w * inv_t;
+            if (s >= thr) {
+                in = true;
+                const float p = deg ? 0.0f : qs_expf_core(s - msc, tab) * inv;
+                key = pid_key(p, i);
+            }
+        }
+        const uint64_t m = __ballot(in);
+        int base = 0;
+        if (lane == 0 && m) base = atomicAdd(&fl.sh[1], __popcll(m));
+        base = __shfl(base, 0, 64);
+        if (in) ka[base + lane_prefix(m)] = key;
+    }
+    __syncthreads();
+    const int nw = fl.sh[1];
+    __syncthreads();
+    const uint64_t *srt = radix_sort_desc<NT>(ka, kb, nw, fl.whist, fl.wsum, &fl.sh[2]);
+    if (tid == 0) {
+        qs_pick_diag d;
+        memset(&d, 0, sizeof d);
+        uint64_t rs = st.rng[row];
+        int id = 0;
+        if (nw == 0) {
+            // empty window: sample.c returns the id its scratch still holds; here 0
+            d.u = rng_unit(rs);
+            d.path = QS_PATH_EMPTY;
+            d.keep = 1;
+        } else {
+            const float qnan = __builtin_nanf("");
+#define QS_PF(i) (deg ? qnan : key_p(srt[(i)]))
+            int n = nw;                                           // sample.c:153-168
+            if (P.top_k > 0 && P.top_k < n) n = P.top_k;
+            d.keep_topk = n;
+            if (P.top_p < 1.0f) {
+                double cum = 0.0;
+                int keep = n;
+                for (int i = 0; i < n; ++i) {
+                    cum += QS_PF(i);
+                    if (cum >= P.top_p) { keep = i + 1; break; }
+                }
+                n = keep;
+            }
+            d.keep_topp = n;
+            if (P.min_p > 0.0f) {
+                const float floor_p = P.min_p * QS_PF(0);
+                int keep = n;
+                for (int i = 1; i < n; ++i)
+                    if (QS_PF(i) < floor_p) { keep = i; break; }
+                n = keep;
+            }
+            if (n < 1) n = 1;
+            double rsum = 0.0;                                    // sample.c:170-175
+            for (int i = 0; i < n; ++i) rsum += QS_PF(i);
+            const double u = rng_unit(rs);
+            const double r = u * rsum;
+            double acc = 0.0;
+            int rank = n - 1;
+            for (int i = 0; i < n; ++i) {
+                acc += QS_PF(i);
+                if (r <= acc) { rank = i; break; }
+            }
+            id = key_id(srt[rank]);
+            d.keep = n;
+            d.rank = rank;
+            d.rsum = rsum;
+            d.u = u;
+            d.p0 = QS_PF(0);
+#undef QS_PF
+            d.path = QS_PATH_FULL;
+        }
+        st.rng[row] = rs;
+        ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
+        out[row] = id;
+        d.id = id;
+        d.n_window = nw;
+        d.n_cand = nw;
+        d.maxl = maxl;
+        d.msc = msc;
+        d.inv = deg ? __builtin_nanf("") : inv;
+        d.sum = deg ? (double)__builtin_nanf("") : sum;
+        if (diag) diag[row] = d;
+        __threadfence();
+        atomicExch(&sc.locks[slot], 0);
+    }
+    __syncthreads();
+}
+
+}  // namespace qs
