@@ -13,7 +13,7 @@ Also reported on the same JSON line:
   cpu_baseline  the reference's own sample.c (oracle/_ref, when built) or the CPU
                 restatement, on this host's cores, over a bounded sample of the same rows
   parity        the first step's ids against the CPU on every sampled row
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--mode M]
 """
 import argparse
 import json
@@ -40,6 +40,8 @@ def parse():
                     help="approximate CPU work for the baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: all host cores (<= 16)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", choices=["auto", "split", "pipelined"], default="auto",
+                    help="which kernels a pick uses (qs_batch_set_mode)")
     return ap.parse_args()
 
 
@@ -98,6 +100,8 @@ def main():
     seeds = orc.gen_row_seeds(w.seed, 0, B)
     hist = orc.gen_hist(w.seed, 0, B, w.hist_len, V, w.hist_pool) if w.hist_len else None
     batch = qa.Batch(B, V, max(1, w.repeat_last_n))
+    batch.set_mode({"auto": qa.MODE_AUTO, "split": qa.MODE_SPLIT,
+                    "pipelined": qa.MODE_PIPELINED}[args.mode])
     batch.config(0, B, *w.params(), seeds=seeds)
     if hist is not None:
         batch.set_history(0, hist)
@@ -143,10 +147,11 @@ def main():
         "config": {"workload": w.name, "batch": B, "vocab": V, "history": w.hist_len,
                    "temperature": w.temperature, "top_k": w.top_k, "top_p": w.top_p,
                    "min_p": w.min_p, "repeat_penalty": w.repeat_penalty,
-                   "description": w.description},
+                   "mode": args.mode, "description": w.description},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "one pick (k_scan + k_expsum + k_finalize + k_full)",
+                     "kernel": ("one pick (k_pipe)" if args.mode == "pipelined" else
+                                "one pick (k_scan + k_expsum + k_finalize)"),
                      "bytes_per_step": alg_bytes},
         "cpu_baseline": cpu,
         "parity": parity,

@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libquasar_sampler.so")
 
 QS_EINVAL, QS_ENOMEM, QS_EDEVICE = -22, -12, -5
 PATH_GREEDY, PATH_FAST, PATH_FULL, PATH_EMPTY = 0, 1, 2, 3
+MODE_AUTO, MODE_SPLIT, MODE_PIPELINED = 0, 1, 2
 
 
 class PickDiag(C.Structure):
@@ -38,6 +39,7 @@ PROTOS = [
     ("qs_batch_set_history", _i, [_vp, _i, _i, C.POINTER(C.c_int32), _i]),
     ("qs_batch_pick", _i, [_vp, _vp, _i64, _i, _i, _vp, _vp]),
     ("qs_batch_set_state", _i, [_vp, _i, _u64, C.POINTER(C.c_int32), _i]),
+    ("qs_batch_set_mode", _i, [_vp, _i]),
     ("qs_batch_synchronize", _i, [_vp]),
     ("qs_batch_get_state", _i, [_vp, _i, C.POINTER(C.c_uint64), C.POINTER(C.c_int32), _i,
                                 C.POINTER(C.c_int)]),

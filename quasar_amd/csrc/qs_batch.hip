@@ -40,6 +40,7 @@
 #include "qs_expf.h"
 #include "qs_gen.h"
 #include "qs_internal.h"
+#include "qs_launch.h"
 
 using namespace qs;
 
@@ -297,13 +298,11 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
     __shared__ uint32_t keys[FIN_CAP];
     __shared__ int32_t ids[FIN_CAP];
     __shared__ uint64_t srt[SORT_CAP];
-    __shared__ uint64_t tab[QS_EXPF_TAB_N];
-    __shared__ uint32_t hist[256];
     __shared__ int offs[S_MAX + 1];
-    __shared__ int sh[8];
-    __shared__ uint32_t shu[2];
-    __shared__ float shf[2];
-    __shared__ double shd[1];
+    __shared__ RowTotals tot;
+    __shared__ float gbv;
+    __shared__ int gbi;
+    __shared__ DecideLds<WG> dl;
     __shared__ FullLds<WG> fl;
 
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -313,8 +312,7 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
     const qs_row_param P = st.prm[row];
     const int S = g.slices;
     const int l0 = row * S;
-    int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
-    if (tid < QS_EXPF_TAB_N) tab[tid] = c_exp_tab[tid];
+    if (tid < QS_EXPF_TAB_N) dl.tab[tid] = c_exp_tab[tid];
 
     // Row totals from the S slices (wave 0; S <= 64).  The double sum is a fixed
     // butterfly over slice positions, so it does not depend on timing.
@@ -326,7 +324,7 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
             float bv = have ? sc.bestv[l0 + lane] : -INFINITY;
             int bi = have ? sc.besti[l0 + lane] : -1;
             wave_best(bv, bi);
-            if (lane == 0) { sh[0] = bi; shf[0] = mx; }
+            if (lane == 0) { gbv = bv; gbi = bi; tot.maxl = mx; }
         } else {
             double ps = have ? sc.psum[l0 + lane] : 0.0;
             int pc = have ? sc.pcnt[l0 + lane] : 0;
@@ -345,74 +343,24 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
             if (have) offs[lane] = incl - cc;
             if (lane == 63) offs[S] = incl;
             if (lane == 0) {
-                shf[0] = mx;
-                shd[0] = ps;
-                sh[1] = pc;
-                sh[2] = cf;
-                shu[0] = cr;
+                tot.maxl = mx;
+                tot.sum = ps;
+                tot.nwin = pc;
+                tot.cflag = cf;
+                tot.rej = cr;
             }
         }
     }
     __syncthreads();
-    const float maxl = shf[0];
-
-    if (row_greedy(P)) {                                   // sample.c:130-134
-        if (tid == 0) {
-            // sample.c scans from index 0 with a strict '>': nothing beats a NaN at 0, and
-            // a row with nothing above -inf stays at 0.
-            const float x0 = g.logits[(int64_t)row * g.stride];
-            const int i0 = sh[0];
-            const int id = (i0 < 0 || isnan(x0)) ? 0 : i0;
-            ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
-            a.out[row] = id;
-            if (a.diag) {
-                qs_pick_diag d;
-                memset(&d, 0, sizeof d);
-                d.id = id;
-                d.path = QS_PATH_GREEDY;
-                d.maxl = maxl;
-                d.keep = 1;
-                a.diag[row] = d;
-            }
-        }
-        return;
-    }
-
-    const double sum = shd[0];
-    const int nwin = sh[1];
-    const float inv_t = P.inv_t;
-    const float msc = maxl * inv_t;
-    const float thr = msc - 30.0f;
     const float *x = g.logits + (int64_t)row * g.stride;
-    if (isnan(msc)) {
-        // Empty window (thr is NaN): sample.c returns the id its scratch still holds; 0 here.
-        if (tid == 0) {
-            uint64_t rs = st.rng[row];
-            const double u = rng_unit(rs);
-            st.rng[row] = rs;
-            ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, 0);
-            a.out[row] = 0;
-            if (a.diag) {
-                qs_pick_diag d;
-                memset(&d, 0, sizeof d);
-                d.path = QS_PATH_EMPTY;
-                d.u = u;
-                d.maxl = maxl;
-                d.msc = msc;
-                d.keep = 1;
-                a.diag[row] = d;
-            }
-        }
+    if (row_greedy(P)) {                                   // sample.c:130-134
+        if (tid == 0) record_greedy(row, P, gbv, gbi, tot.maxl, x[0], st, a.out, a.diag);
         return;
     }
-    const int total = offs[S];
-    bool full = !isfinite(msc) || sh[2] != 0 || total > FIN_CAP;
-    uint32_t rej = shu[0];
-    int nkept = 0;
-    __syncthreads();
-    if (!full) {
-        // gather the slice lists
-        for (int s = 0; s < S; ++s) {
+    RowTotals t = tot;
+    t.total = offs[S];
+    if (t.total <= FIN_CAP && isfinite(t.maxl * P.inv_t)) {
+        for (int s = 0; s < S; ++s) {                      // gather the slice lists
             const int o = offs[s], c = offs[s + 1] - o;
             const uint32_t *gk = sc.ckey + (int64_t)(l0 + s) * sc.ccap;
             const int32_t *gi = sc.cid + (int64_t)(l0 + s) * sc.ccap;
@@ -421,90 +369,10 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
                 ids[o + j] = gi[j];
             }
         }
-        __syncthreads();
-        // the row's top K by logit (ties kept); everything dropped raises `rej`
-        const int K = row_ksel(P);
-        const uint32_t th = total > K ? block_kth<WG>(keys, total, K, hist, sh + 4) : 0u;
-        if (tid == 0) sh[3] = 0;
-        __syncthreads();
-        const float inv = (float)(1.0 / sum);
-        uint32_t myrej = 0u;
-        for (int j0 = 0; j0 < total; j0 += WG) {
-            const int j = j0 + tid;
-            const bool valid = j < total;
-            const uint32_t k = valid ? keys[j] : 0u;
-            const bool keep = valid && k >= th;
-            if (valid && !keep) myrej = k > myrej ? k : myrej;
-            const uint64_t m = __ballot(keep);
-            int wbase = 0;
-            if (lane == 0 && m) wbase = atomicAdd(&sh[3], __popcll(m));
-            wbase = __shfl(wbase, 0, 64);
-            if (keep) {
-                const int pos = wbase + lane_prefix(m);
-                if (pos < SORT_CAP) {
-                    const float s = key2f(k) * inv_t;
-                    uint64_t key = 0ull;               // out of the window: sorts last
-                    if (s >= thr) key = pid_key(qs_expf_core(s - msc, tab) * inv, ids[j]);
-                    srt[pos] = key;
-                }
-            }
-        }
-        myrej = wave_max_u(myrej);
-        if (lane == 0) atomicMax(&shu[0], myrej);
-        __syncthreads();
-        nkept = sh[3];
-        rej = shu[0];
-        if (nkept > SORT_CAP) full = true;
     }
-    if (!full) {
-        int npad = 1;
-        while (npad < nkept) npad <<= 1;
-        for (int j = nkept + tid; j < npad; j += WG) srt[j] = 0ull;
-        __syncthreads();
-        bitonic_desc<WG>(srt, npad);
-        if (tid == 0) {
-            const float inv = (float)(1.0 / sum);
-            int m = 0;                         // in-window candidates (p > 0) sort first
-            while (m < nkept && (srt[m] >> 32) != 0ull) ++m;
-            // The largest probability any rejected logit can have (p is monotone in it).
-            float p_rej = -1.0f;
-            if (rej > KEY_NEG_INF) {
-                const float s = key2f(rej) * inv_t;
-                if (s >= thr) p_rej = qs_expf_core(s - msc, tab) * inv;
-            }
-            // Positions [0, E) of the sorted candidates are positions of the full order.
-            int E = m;
-            if (m < nwin)
-                for (int i = 0; i < m; ++i)
-                    if (key_p(srt[i]) <= p_rej) { E = i; break; }
-            qs_pick_diag d;
-            memset(&d, 0, sizeof d);
-            uint64_t rs = st.rng[row];
-            int id = -1;
-            if (decide_prefix(srt, E, nwin, P, rs, id, d)) {
-                st.rng[row] = rs;
-                ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
-                a.out[row] = id;
-                if (a.diag) {
-                    d.id = id;
-                    d.path = QS_PATH_FAST;
-                    d.n_window = nwin;
-                    d.n_cand = m;
-                    d.maxl = maxl;
-                    d.msc = msc;
-                    d.inv = inv;
-                    d.sum = sum;
-                    a.diag[row] = d;
-                }
-                sh[0] = 0;
-            } else {
-                sh[0] = 1;
-            }
-        }
-        __syncthreads();
-        full = sh[0] != 0;
-    }
-    if (full) full_row<WG>(x, g.vocab, row, P, maxl, sum, st, sc, a.out, a.diag, tab, fl);
+    __syncthreads();
+    decide_row<WG>(row, P, t, FIN_CAP, keys, ids, srt, dl, fl, x, g.vocab, st, sc, a.out,
+                   a.diag, -1);
 }
 
 // ---- synthetic inputs and the expf check ---------------------------------------------------
@@ -567,6 +435,8 @@ int slices_for(int n_rows, int vocab, int kmax_sel, int *slice_len) {
 
 struct qs_batch {
     int max_rows = 0, max_vocab = 0, max_last_n = 0;
+    int mode = QS_MODE_AUTO;               // QS_MODE_*: which kernels a pick uses
+    int pipe_grid = 0;                     // persistent workgroups of the pipelined kernel
     int slice_rows = 0;                    // capacity of the per-slice scratch (rows*S)
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -583,7 +453,8 @@ static void batch_release(qs_batch *b) {
     void *ptrs[] = {b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead, b->sc.smax,
                     b->sc.bestv, b->sc.besti, b->sc.sth, b->sc.ckey, b->sc.cid, b->sc.ccnt,
                     b->sc.crej, b->sc.cflag, b->sc.psum, b->sc.pcnt, b->sc.locks,
-                    b->sc.full_keys, b->sc.full_bm, b->sc.err};
+                    b->sc.full_keys, b->sc.full_bm, b->sc.err, b->sc.rowmax, b->sc.arrive,
+                    b->sc.done};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     if (b->ev0) (void)hipEventDestroy(b->ev0);
@@ -598,8 +469,19 @@ static int batch_alloc(qs_batch *b) {
     int sr = R;
     const int many = TARGET_WGS < S_MAX * R ? TARGET_WGS : S_MAX * R;
     if (many > sr) sr = many;
+    if (qs_pipe_parts() * R > sr) sr = qs_pipe_parts() * R;   // pipelined kernel: per part
     b->slice_rows = sr;
-    b->sc.nslots = R < SLOTS ? R : SLOTS;
+    int dev = 0, ncu = 0, coop = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess) {
+        qs_set_error("device attributes unavailable");
+        return QS_EDEVICE;
+    }
+    b->pipe_grid = coop ? ncu / qs_pipe_parts() * qs_pipe_parts() : 0;
+    int slots = R < SLOTS ? R : SLOTS;
+    if (b->pipe_grid > 0 && R > slots) slots = R < b->pipe_grid ? R : b->pipe_grid;
+    b->sc.nslots = slots;
     b->sc.ccap = CCAP;
     int rc = 0;
     if (!rc) rc = dev_alloc(&b->d_prm, R, "params");
@@ -622,6 +504,12 @@ static int batch_alloc(qs_batch *b) {
     if (!rc) rc = dev_alloc(&b->sc.full_keys, (size_t)b->sc.nslots * 2 * V, "full_keys");
     if (!rc) rc = dev_alloc(&b->sc.full_bm, (size_t)b->sc.nslots * (V / 32 + 1), "full_bm");
     if (!rc) rc = dev_alloc(&b->sc.err, 1, "err");
+    if (!rc) rc = dev_alloc(&b->sc.rowmax, R, "rowmax");
+    if (!rc) rc = dev_alloc(&b->sc.arrive, R, "arrive");
+    if (!rc) rc = dev_alloc(&b->sc.done, R, "done");
+    if (!rc && hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * R) != hipSuccess) rc = QS_EDEVICE;
+    if (!rc && hipMemset(b->sc.arrive, 0, sizeof(int32_t) * R) != hipSuccess) rc = QS_EDEVICE;
+    if (!rc && hipMemset(b->sc.done, 0, sizeof(int32_t) * R) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.locks, 0, sizeof(int32_t) * b->sc.nslots) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.err, 0, sizeof(int32_t)) != hipSuccess) rc = QS_EDEVICE;
     return rc;
@@ -796,6 +684,18 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
         if (k > kmax) kmax = k;
         if (p.ring_cap > b->max_last_n) { qs_set_error("ring capacity"); return QS_EINVAL; }
     }
+    RowState st0{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
+                 b->max_last_n > 0 ? b->max_last_n : 1};
+    const bool pipe_ok = b->pipe_grid > 0 && kmax <= K_MAX &&
+                         qs_pipe_supported(n_rows, n_vocab, row_stride, d_logits, b->pipe_grid);
+    if (b->mode == QS_MODE_PIPELINED && !pipe_ok) {
+        qs_set_error("qs_batch_pick: the pipelined kernel does not support this pick");
+        return QS_EINVAL;
+    }
+    if (b->mode == QS_MODE_PIPELINED) {
+        return qs_pipe_launch(d_logits, row_stride, n_rows, n_vocab, st0, b->sc, d_out, d_diag,
+                              b->pipe_grid, b->stream);
+    }
     Geometry g;
     g.logits = d_logits;
     g.stride = row_stride;
@@ -833,13 +733,29 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
     return 0;
 }
 
+int qs_batch_set_mode(qs_batch *b, int mode) {
+    if (!b || mode < QS_MODE_AUTO || mode > QS_MODE_PIPELINED) {
+        qs_set_error("qs_batch_set_mode: bad mode %d", mode);
+        return QS_EINVAL;
+    }
+    b->mode = mode;
+    return 0;
+}
+
 int qs_batch_synchronize(qs_batch *b) {
     if (!b) return QS_EINVAL;
     HIP_TRY(hipStreamSynchronize(b->stream), "qs_batch_synchronize");
     int32_t err = 0;
     HIP_TRY(hipMemcpy(&err, b->sc.err, sizeof err, hipMemcpyDeviceToHost), "error flag");
     if (err) {
-        qs_set_error("a row waited too long for full-window scratch (id -3 returned)");
+        // clear the flag and the pipelined kernel's counters so the next pick starts clean
+        const int32_t zero = 0;
+        (void)hipMemcpy(b->sc.err, &zero, sizeof zero, hipMemcpyHostToDevice);
+        (void)hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * b->max_rows);
+        (void)hipMemset(b->sc.arrive, 0, sizeof(int32_t) * b->max_rows);
+        (void)hipMemset(b->sc.done, 0, sizeof(int32_t) * b->max_rows);
+        qs_set_error("a bounded wait on the device gave up (flags %d); the rows involved "
+                     "returned wrong ids", err);
         return QS_EDEVICE;
     }
     return 0;

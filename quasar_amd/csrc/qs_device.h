@@ -149,6 +149,9 @@ struct Scratch {
     uint64_t *full_keys;  // [nslots][2][vocab]
     uint32_t *full_bm;    // [nslots][vocab/32+1]
     int32_t *err;         // [1] sticky error flag (bounded wait gave up)
+    uint32_t *rowmax;     // [rows] pipelined kernel: row max key, combined by atomicMax
+    int32_t *arrive;      // [rows] pipelined kernel: parts whose max is published
+    int32_t *done;        // [rows] pipelined kernel: parts whose sums/candidates are written
     int nslots;
     int ccap;             // candidates per slice list
 };
@@ -166,7 +169,7 @@ struct Geometry {
 // History membership of [lo, hi) as a bitmap (LDS or global); ids outside are skipped and
 // duplicates set the same bit, so each id is penalised once (sample.c:120).
 template <int NT>
-__device__ void build_bitmap(uint32_t *bm, int words, int lo, int hi, const RowState &st,
+__device__ __forceinline__ void build_bitmap(uint32_t *bm, int words, int lo, int hi, const RowState &st,
                              int row, int cap) {
     for (int j = threadIdx.x; j < words; j += NT) bm[j] = 0u;
     __syncthreads();
@@ -199,7 +202,7 @@ __device__ __forceinline__ float4 load4(const float *x, int c, int hi) {
 // K-th largest of n keys in LDS (1 <= k <= n), by 8-bit radix select: four rounds of a
 // 256-bin histogram restricted to the prefix found so far.
 template <int NT>
-__device__ uint32_t block_kth(const uint32_t *keys, int n, int k, uint32_t *hist, int *sh) {
+__device__ __forceinline__ uint32_t block_kth(const uint32_t *keys, int n, int k, uint32_t *hist, int *sh) {
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t prefix = 0u, pmask = 0u;
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -243,7 +246,7 @@ __device__ uint32_t block_kth(const uint32_t *keys, int n, int k, uint32_t *hist
 
 // Sort n_pad (a power of two) 64-bit keys in LDS, descending.
 template <int NT>
-__device__ void bitonic_desc(uint64_t *s, int n_pad) {
+__device__ __forceinline__ void bitonic_desc(uint64_t *s, int n_pad) {
     for (int size = 2; size <= n_pad; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             for (int i = threadIdx.x; i < (n_pad >> 1); i += NT) {
@@ -272,7 +275,7 @@ __device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)(k & 
 // hold in-window candidates; positions [0, E) are known to be positions of the full
 // order.  nwin is the window size.  Returns false (nothing consumed) when the cuts or the
 // draw would read a position >= E; otherwise advances rs and fills id and d.
-__device__ bool decide_prefix(const uint64_t *srt, int E, int nwin, const qs_row_param &P,
+__device__ __forceinline__ bool decide_prefix(const uint64_t *srt, int E, int nwin, const qs_row_param &P,
                               uint64_t &rs, int &id, qs_pick_diag &d) {
     if (E < 1) return false;
     int n = nwin;                                             // sample.c:153-154
@@ -325,7 +328,7 @@ __device__ bool decide_prefix(const uint64_t *srt, int E, int nwin, const qs_row
 // owns a contiguous range and ranks equal digits by lane order (ballot multisplit).
 // Returns the buffer holding the result (a or b).  whist: NT/64*256 words, sh: 1 int.
 template <int NT>
-__device__ uint64_t *radix_sort_desc(uint64_t *a, uint64_t *b, int n, uint32_t *whist,
+__device__ __forceinline__ uint64_t *radix_sort_desc(uint64_t *a, uint64_t *b, int n, uint32_t *whist,
                                      uint32_t *wsum, int *sh) {
     constexpr int NWV = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -407,18 +410,21 @@ struct FullLds {
 // Takes a scratch slot (bounded wait; on giving up the row gets id -3 and the sticky error
 // flag is set).  maxl/sum/nwin are the row totals of the two streaming passes.
 template <int NT>
-__device__ void full_row(const float *x, int V, int row, const qs_row_param &P, float maxl,
+__device__ __forceinline__ void full_row(const float *x, int V, int row, const qs_row_param &P, float maxl,
                          double sum, const RowState &st, const Scratch &sc, int32_t *out,
-                         qs_pick_diag *diag, const uint64_t *tab, FullLds<NT> &fl) {
+                         qs_pick_diag *diag, const uint64_t *tab, FullLds<NT> &fl,
+                         int fixed_slot) {
     const int tid = threadIdx.x, lane = tid & 63;
     int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+    const bool locked = fixed_slot < 0;
     if (tid == 0) {
-        int slot = -1;
-        for (int it = 0; it < SPIN_LIMIT; ++it) {
-            const int s = (row + it) % sc.nslots;
-            if (atomicCAS(&sc.locks[s], 0, 1) == 0) { slot = s; break; }
-            if ((it + 1) % sc.nslots == 0) __builtin_amdgcn_s_sleep(16);
-        }
+        int slot = fixed_slot;
+        if (locked)
+            for (int it = 0; it < SPIN_LIMIT; ++it) {
+                const int s = (row + it) % sc.nslots;
+                if (atomicCAS(&sc.locks[s], 0, 1) == 0) { slot = s; break; }
+                if ((it + 1) % sc.nslots == 0) __builtin_amdgcn_s_sleep(16);
+            }
         fl.sh[0] = slot;
     }
     __syncthreads();
@@ -533,10 +539,181 @@ __device__ void full_row(const float *x, int V, int row, const qs_row_param &P, 
         d.inv = deg ? __builtin_nanf("") : inv;
         d.sum = deg ? (double)__builtin_nanf("") : sum;
         if (diag) diag[row] = d;
-        __threadfence();
-        atomicExch(&sc.locks[slot], 0);
+        if (locked) {
+            __threadfence();
+            atomicExch(&sc.locks[slot], 0);
+        }
     }
     __syncthreads();
+}
+
+// ---- everything after the two streaming passes, for one sampling row ------------------------
+
+// Row totals gathered from the streaming passes.
+struct RowTotals {
+    float maxl;      // max penalised logit
+    double sum;      // double softmax denominator (fixed-order partial sums)
+    int nwin;        // window size
+    int cflag;       // some candidate list overflowed
+    uint32_t rej;    // bound on every logit not among the candidates (key; 0: none)
+    int total;       // gathered candidates (keys[], ids[])
+};
+
+// LDS a decision needs besides the gathered candidates.
+template <int NT>
+struct DecideLds {
+    uint64_t tab[QS_EXPF_TAB_N];
+    uint32_t hist[256];
+    int sh[8];
+    uint32_t shu[2];
+};
+
+// sample.c:136-178 for a sampling row whose candidates (keys[0..t.total), ids) are in LDS:
+// radix-select the top K by logit, exact p, bitonic sort, prove the prefix, decide and
+// record; rows the proof does not cover go through full_row.  fcap bounds t.total,
+// srt holds SORT_CAP keys.  fixed_slot >= 0 names a full-window scratch slot owned by the
+// caller, -1 takes one under the slot locks.  All threads of the block call this.
+template <int NT>
+__device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const RowTotals &t, int fcap,
+                           uint32_t *keys, int32_t *ids, uint64_t *srt, DecideLds<NT> &dl,
+                           FullLds<NT> &fl, const float *x, int V, const RowState &st,
+                           const Scratch &sc, int32_t *out, qs_pick_diag *diag,
+                           int fixed_slot) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+    const uint64_t *tab = dl.tab;
+    const float inv_t = P.inv_t;
+    const float msc = t.maxl * inv_t;
+    const float thr = msc - 30.0f;
+    if (isnan(msc)) {
+        // Empty window (thr is NaN): sample.c returns the id its scratch still holds; 0 here.
+        if (tid == 0) {
+            uint64_t rs = st.rng[row];
+            const double u = rng_unit(rs);
+            st.rng[row] = rs;
+            ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, 0);
+            out[row] = 0;
+            if (diag) {
+                qs_pick_diag d;
+                memset(&d, 0, sizeof d);
+                d.path = QS_PATH_EMPTY;
+                d.u = u;
+                d.maxl = t.maxl;
+                d.msc = msc;
+                d.keep = 1;
+                diag[row] = d;
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    bool full = !isfinite(msc) || t.cflag != 0 || t.total > fcap;
+    int nkept = 0;
+    uint32_t rej = t.rej;
+    if (!full) {
+        // the row's top K by logit (ties kept); everything dropped raises `rej`
+        const int K = row_ksel(P);
+        const uint32_t th = t.total > K ? block_kth<NT>(keys, t.total, K, dl.hist, dl.sh + 4) : 0u;
+        if (tid == 0) { dl.sh[3] = 0; dl.shu[0] = rej; }
+        __syncthreads();
+        const float inv = (float)(1.0 / t.sum);
+        uint32_t myrej = 0u;
+        for (int j0 = 0; j0 < t.total; j0 += NT) {
+            const int j = j0 + tid;
+            const bool valid = j < t.total;
+            const uint32_t k = valid ? keys[j] : 0u;
+            const bool keep = valid && k >= th;
+            if (valid && !keep) myrej = k > myrej ? k : myrej;
+            const uint64_t m = __ballot(keep);
+            int wbase = 0;
+            if (lane == 0 && m) wbase = atomicAdd(&dl.sh[3], __popcll(m));
+            wbase = __shfl(wbase, 0, 64);
+            if (keep) {
+                const int pos = wbase + lane_prefix(m);
+                if (pos < SORT_CAP) {
+                    const float s = key2f(k) * inv_t;
+                    uint64_t key = 0ull;               // out of the window: sorts last
+                    if (s >= thr) key = pid_key(qs_expf_core(s - msc, tab) * inv, ids[j]);
+                    srt[pos] = key;
+                }
+            }
+        }
+        myrej = wave_max_u(myrej);
+        if (lane == 0) atomicMax(&dl.shu[0], myrej);
+        __syncthreads();
+        nkept = dl.sh[3];
+        rej = dl.shu[0];
+        if (nkept > SORT_CAP) full = true;
+    }
+    if (!full) {
+        int npad = 1;
+        while (npad < nkept) npad <<= 1;
+        for (int j = nkept + tid; j < npad; j += NT) srt[j] = 0ull;
+        __syncthreads();
+        bitonic_desc<NT>(srt, npad);
+        if (tid == 0) {
+            const float inv = (float)(1.0 / t.sum);
+            int m = 0;                         // in-window candidates (p > 0) sort first
+            while (m < nkept && (srt[m] >> 32) != 0ull) ++m;
+            // The largest probability any rejected logit can have (p is monotone in it).
+            float p_rej = -1.0f;
+            if (rej > KEY_NEG_INF) {
+                const float s = key2f(rej) * inv_t;
+                if (s >= thr) p_rej = qs_expf_core(s - msc, tab) * inv;
+            }
+            // Positions [0, E) of the sorted candidates are positions of the full order.
+            int E = m;
+            if (m < t.nwin)
+                for (int i = 0; i < m; ++i)
+                    if (key_p(srt[i]) <= p_rej) { E = i; break; }
+            qs_pick_diag d;
+            memset(&d, 0, sizeof d);
+            uint64_t rs = st.rng[row];
+            int id = -1;
+            if (decide_prefix(srt, E, t.nwin, P, rs, id, d)) {
+                st.rng[row] = rs;
+                ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
+                out[row] = id;
+                if (diag) {
+                    d.id = id;
+                    d.path = QS_PATH_FAST;
+                    d.n_window = t.nwin;
+                    d.n_cand = m;
+                    d.maxl = t.maxl;
+                    d.msc = msc;
+                    d.inv = inv;
+                    d.sum = t.sum;
+                    diag[row] = d;
+                }
+                dl.sh[0] = 0;
+            } else {
+                dl.sh[0] = 1;
+            }
+        }
+        __syncthreads();
+        full = dl.sh[0] != 0;
+        __syncthreads();
+    }
+    if (full) full_row<NT>(x, V, row, P, t.maxl, t.sum, st, sc, out, diag, tab, fl, fixed_slot);
+}
+
+// sample.c:130-134 from per-slice (value, first index) bests: nothing beats a NaN at index
+// 0 and a row with nothing above -inf stays at 0.  One thread.
+__device__ __forceinline__ void record_greedy(int row, const qs_row_param &P, float bv, int bi, float maxl,
+                              float x0, const RowState &st, int32_t *out, qs_pick_diag *diag) {
+    int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+    const int id = (bi < 0 || isnan(x0)) ? 0 : bi;
+    ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
+    out[row] = id;
+    if (diag) {
+        qs_pick_diag d;
+        memset(&d, 0, sizeof d);
+        d.id = id;
+        d.path = QS_PATH_GREEDY;
+        d.maxl = maxl;
+        d.keep = 1;
+        diag[row] = d;
+    }
 }
 
 }  // namespace qs

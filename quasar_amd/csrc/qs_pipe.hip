@@ -1,0 +1,621 @@
+// qs_pipe.hip - the pipelined pick for batches large enough to fill the GPU.
+//
+// One persistent workgroup of 1024 threads per CU (cooperative launch, grid G).  Every row
+// is cut into PARTS = 8 parts; at stage s the grid works on G/PARTS rows, part j of
+// row-in-stage q going to workgroup q + j*G/PARTS (with G a multiple of 64 the eight
+// workgroups of a row are congruent mod 8, i.e. on one XCD when workgroups are dealt to
+// XCDs round-robin).  A part is read from HBM once, straight into registers, and stays
+// there until its softmax terms are summed.
+//
+// Wave 0 is the control wave and never loads logits; waves 1-15 (960 threads, UP float4
+// each) hold data.  Three register buffers rotate: the part being summed (s), the next
+// part, already penalised and published (s+1), and the part after that, loading (s+2).
+// Per stage:
+//
+//   data waves                              control wave
+//   sum(s): w*inv_t, window, libm-equal     publish max(s+1); wait for the row's eight
+//   expf, double partial sums, candidates   maxima of s+1 (bounded); threshold(s+1);
+//   at or above threshold(s)                history bitmap for part s+2
+//   -------------------------------------- barrier --------------------------------------
+//   complete(s+2): penalty, thread maxima,  store part s's sums and candidates, release
+//   part max; issue loads of part s+3       them
+//   -------------------------------------- barrier --------------------------------------
+//
+// so the waits, the threshold select and the stores overlap the data waves' work, and a
+// wave's memory counter never covers another wave's loads.  After the last stage each
+// workgroup finishes rows r = w (mod G) with decide_row (k_finalize's logic), using its
+// own full-window scratch slot.
+//
+// Every wait is bounded (SPIN_LIMIT polls): one that gives up sets the sticky error flag
+// and the pick reports an error instead of hanging.  A workgroup only waits for
+// publications that its partners make before they wait on anything later, and the
+// cooperative launch keeps every workgroup resident, so the waits end.
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#include "../../include/quasar_sampler.h"
+#include "qs_device.h"
+#include "qs_launch.h"
+
+using namespace qs;
+
+namespace {
+
+constexpr int NT = 1024;             // threads per workgroup
+constexpr int NWV = NT / 64;         // wavefronts
+constexpr int DT = NT - 64;          // data threads (waves 1..15)
+constexpr int PARTS = 8;             // parts per row
+constexpr int UP = 5;                // float4 per data thread per part
+constexpr int PCAP = 2048;           // candidates per part (== Scratch::ccap)
+constexpr int FCAP = 4096;           // candidates gathered per row in the epilogue
+
+__constant__ uint64_t c_exp_tab_p[QS_EXPF_TAB_N] = QS_EXPF_TABLE_INIT;
+
+struct PipeArgs {
+    const float *logits;
+    int64_t stride;
+    int vocab;
+    int n_rows;
+    int part_len;                    // elements per part (multiple of 4)
+    int stages;
+    RowState st;
+    Scratch sc;
+    int32_t *out;
+    qs_pick_diag *diag;
+};
+
+// Shared state of one workgroup besides the dynamic region.
+struct PipeLds {
+    DecideLds<NT> dl;
+    float wmax[NWV];                 // per-wave part max of the part being completed
+    float wbv[NWV];                  // greedy: per-wave best value / index
+    int wbi[NWV];
+    double wsum[NWV];                // per-wave partial sums of the part being summed
+    int wcnt[NWV];                   // per-wave window counts
+    int wovf;                        // candidate buffer overflowed
+    int ncand;                       // candidates in the LDS buffer
+    uint32_t maxkey[2];              // row max key of parts s and s+1, by stage parity
+    uint32_t theta[2];               // candidate threshold keys, by stage parity
+    RowTotals tot;
+    int offs[PARTS + 1];
+    float gbv;
+    int gbi;
+};
+
+struct Geo {                         // this workgroup's part of every row
+    int part, c_lo, c_hi, lo, rps, bm_words;
+};
+
+__device__ __forceinline__ int task_row(int s, int w, int rps) { return s * rps + (w % rps); }
+
+__device__ __forceinline__ bool task_valid(const PipeArgs &a, int s, const Geo &g, int w) {
+    return s < a.stages && task_row(s, w, g.rps) < a.n_rows;
+}
+
+// Data waves: loads of one part into registers (float4 c = c_lo + u*DT + dt; lanes past
+// the part read the part's last float4, and are masked later).
+__device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a, int row,
+                                            const Geo &g) {
+    const float4 *x4 = (const float4 *)(a.logits + (int64_t)row * a.stride);
+    const int dt = (int)threadIdx.x - 64;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+        const int c = g.c_lo + u * DT + dt;
+        buf[u] = x4[c < g.c_hi ? c : g.c_hi - 1];
+    }
+}
+
+// Data waves: penalty, thread maxima (into tm), per-wave part max (greedy: best).
+__device__ __forceinline__ void complete_part(float4 (&buf)[UP], const PipeArgs &a, int row,
+                                              const Geo &g, const uint32_t *bm, uint32_t *tm,
+                                              PipeLds &pl) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const qs_row_param P = a.st.prm[row];
+    const float rp = P.repeat_penalty;
+    const bool pen = rp > 1.0f && a.st.hlen[row] > 0 && P.ring_cap > 0;
+    const bool greedy = row_greedy(P);
+    const float qnan = __builtin_nanf("");
+    float mx = -INFINITY, bv = -INFINITY;
+    int bi = -1;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+        const int c = g.c_lo + u * DT + (tid - 64);
+        float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
+        if (c >= g.c_hi) w[0] = w[1] = w[2] = w[3] = qnan;
+        if (pen) {
+            uint32_t nib = 0u;
+            if (c < g.c_hi) {
+                const int r = 4 * c - g.lo;
+                nib = (bm[r >> 5] >> (r & 31)) & 0xFu;
+            }
+            if (__ballot(nib != 0u)) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if ((nib >> k) & 1u) w[k] = penalise(w[k], rp);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) mx = w[k] > mx ? w[k] : mx;
+        if (greedy) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (w[k] > bv) { bv = w[k]; bi = 4 * c + k; }
+        }
+        buf[u] = make_float4(w[0], w[1], w[2], w[3]);
+    }
+    tm[tid - 64] = f2key(mx);
+    const float m = wave_max_f(mx);
+    if (greedy) wave_best(bv, bi);
+    if (lane == 0) {
+        pl.wmax[wv] = m;
+        pl.wbv[wv] = bv;
+        pl.wbi[wv] = bi;
+    }
+}
+
+// Data waves: exact softmax numerators, partial sums, window count and candidates of one
+// part, from registers (sample.c:136-149 per element).
+__device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const PipeArgs &a, int row,
+                                         const Geo &g, uint32_t *ckey, int32_t *cid,
+                                         uint32_t maxkey, uint32_t th, PipeLds &pl) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const qs_row_param P = a.st.prm[row];
+    const float inv_t = P.inv_t;
+    const float msc = key2f(maxkey) * inv_t;
+    const float thr = msc - 30.0f;
+    if (row_greedy(P) || !isfinite(msc)) return;   // decided in the epilogue
+    const float thf = th > KEY_NEG_INF ? key2f(th) : -INFINITY;
+    const uint64_t *tab = pl.dl.tab;
+    double acc = 0.0;
+    int cnt = 0;
+    int ovf = 0;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+        const int c = g.c_lo + u * DT + (tid - 64);
+        const bool valid = c < g.c_hi;
+        const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
+        float s[4];
+        bool in[4], cand[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s[k] = w[k] * inv_t;
+            in[k] = valid && s[k] >= thr;
+            cand[k] = valid && w[k] >= thf;
+            cnt += __popcll(__ballot(in[k]));
+        }
+        if (__ballot(in[0] | in[1] | in[2] | in[3])) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float e = qs_expf_core(s[k] - msc, tab);
+                acc += in[k] ? (double)e : 0.0;
+            }
+        }
+        if (__ballot(cand[0] | cand[1] | cand[2] | cand[3])) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint64_t mk = __ballot(cand[k]);
+                if (mk) {
+                    int base = 0;
+                    if (lane == 0) base = atomicAdd(&pl.ncand, __popcll(mk));
+                    base = __shfl(base, 0, 64);
+                    if (cand[k]) {
+                        const int pos = base + lane_prefix(mk);
+                        if (pos < PCAP) {
+                            ckey[pos] = f2key(w[k]);
+                            cid[pos] = 4 * c + k;
+                        } else {
+                            ovf = 1;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    const double sa = wave_sum_d(acc);
+    const int o = wave_or_i(ovf);
+    if (lane == 0) {
+        pl.wsum[wv] = sa;
+        pl.wcnt[wv] = cnt;             // the wave's count (sum of ballot popcounts)
+        if (o) pl.wovf = 1;
+    }
+}
+
+// Control wave: wait (bounded) until all parts of `row` published their max; its key.
+__device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key = 0u;
+    if (lane == 0) {
+        int it = 0;
+        while (__hip_atomic_load(&a.sc.arrive[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+               PARTS) {
+            if (++it >= SPIN_LIMIT) {
+                atomicOr(a.sc.err, 2);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        key = __hip_atomic_load(&a.sc.rowmax[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return __shfl(key, 0, 64);
+}
+
+// Control wave: a candidate threshold for n keys in LDS: the k-th largest key with its
+// low 16 bits cleared (so at least k keys reach it).  Bit-serial over the top 16 bits,
+// counting with ballots, so the counts never leave the scalar unit.
+__device__ __forceinline__ uint32_t wave_kth16_lds(const uint32_t *keys, int n, int k) {
+    const int lane = threadIdx.x & 63;
+    constexpr int PER = DT / 64;       // keys per lane (n <= DT)
+    uint32_t v[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int i = j * 64 + lane;
+        v[j] = i < n ? keys[i] : 0u;
+    }
+    uint32_t prefix = 0u;
+    for (int b = 31; b >= 16; --b) {
+        const uint32_t cand = prefix | (1u << b);
+        int c = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) c += __popcll(__ballot(v[j] >= cand));
+        if (c >= k) prefix = cand;
+    }
+    return prefix;
+}
+
+// Control wave: the history ids of `row` (up to RING_PF per lane stay in registers, so
+// their loads overlap the control wave's other waits) and the bitmap they set.
+constexpr int RING_PF = 8;
+struct RingIds {
+    int id[RING_PF];
+    int len, head, cap;
+    bool pen;
+};
+
+__device__ __forceinline__ RingIds ring_fetch(const PipeArgs &a, int row) {
+    const int lane = threadIdx.x & 63;
+    RingIds r;
+    const RowState &st = a.st;
+    const qs_row_param P = st.prm[row];
+    r.len = st.hlen[row];
+    r.head = st.hhead[row];
+    r.cap = P.ring_cap;
+    r.pen = P.repeat_penalty > 1.0f && r.len > 0 && r.cap > 0;
+    const int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+#pragma unroll
+    for (int q = 0; q < RING_PF; ++q) {
+        const int j = q * 64 + lane;
+        r.id[q] = (r.pen && j < r.len) ? ring[(r.head + j) % r.cap] : -1;
+    }
+    return r;
+}
+
+__device__ __forceinline__ void bitmap_build(uint32_t *bm, const RingIds &r, const PipeArgs &a,
+                                             int row, const Geo &g) {
+    const int lane = threadIdx.x & 63;
+    if (!r.pen) return;
+    for (int j = lane; j < g.bm_words; j += 64) bm[j] = 0u;
+    const int hi = g.c_hi * 4;
+#pragma unroll
+    for (int q = 0; q < RING_PF; ++q) {
+        const int id = r.id[q];
+        if (id >= g.lo && id < hi) atomicOr(&bm[(id - g.lo) >> 5], 1u << ((id - g.lo) & 31));
+    }
+    if (r.len > RING_PF * 64) {                     // longer histories: the rest directly
+        const int32_t *ring = a.st.ring + (int64_t)row * a.st.ring_stride;
+        for (int j = RING_PF * 64 + lane; j < r.len; j += 64) {
+            const int id = ring[(r.head + j) % r.cap];
+            if (id >= g.lo && id < hi) atomicOr(&bm[(id - g.lo) >> 5], 1u << ((id - g.lo) & 31));
+        }
+    }
+}
+
+__device__ __forceinline__ void control_bitmap(uint32_t *bm, const PipeArgs &a, int row,
+                                               const Geo &g) {
+    const RingIds r = ring_fetch(a, row);
+    bitmap_build(bm, r, a, row, g);
+}
+
+// Control wave: publish the completed part's max (sampling) or best (greedy).
+__device__ __forceinline__ void control_publish(const PipeArgs &a, int row, const Geo &g,
+                                                PipeLds &pl) {
+    const int lane = threadIdx.x & 63;
+    if (lane != 0) return;
+    const qs_row_param P = a.st.prm[row];
+    const int li = row * PARTS + g.part;
+    if (row_greedy(P)) {
+        float v0 = pl.wbv[1];
+        int i0 = pl.wbi[1];
+        for (int k = 2; k < NWV; ++k) best_combine(v0, i0, pl.wbv[k], pl.wbi[k]);
+        a.sc.bestv[li] = v0;
+        a.sc.besti[li] = i0;
+        __hip_atomic_fetch_add(&a.sc.done[row], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    float t = pl.wmax[1];
+    for (int k = 2; k < NWV; ++k) t = fmaxf(t, pl.wmax[k]);
+    __hip_atomic_fetch_max(&a.sc.rowmax[row], f2key(t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(&a.sc.arrive[row], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Control wave: store a summed part's results and release them.
+__device__ __forceinline__ void control_store(const PipeArgs &a, int row, const Geo &g,
+                                              uint32_t maxkey, uint32_t th,
+                                              const uint32_t *ckey, const int32_t *cid,
+                                              PipeLds &pl) {
+    const int lane = threadIdx.x & 63;
+    const qs_row_param P = a.st.prm[row];
+    if (row_greedy(P)) return;                    // published with its best already
+    const int li = row * PARTS + g.part;
+    const bool live = isfinite(key2f(maxkey) * P.inv_t);
+    const int n = live ? min(pl.ncand, PCAP) : 0;
+    uint32_t *gk = a.sc.ckey + (int64_t)li * PCAP;
+    int32_t *gi = a.sc.cid + (int64_t)li * PCAP;
+    for (int j = lane; j < n; j += 64) {
+        gk[j] = ckey[j];
+        gi[j] = cid[j];
+    }
+    if (lane == 0) {
+        double t = 0.0;
+        int ct = 0;
+        if (live)
+            for (int k = 1; k < NWV; ++k) {
+                t += pl.wsum[k];
+                ct += pl.wcnt[k];
+            }
+        a.sc.psum[li] = t;
+        a.sc.pcnt[li] = ct;
+        a.sc.ccnt[li] = n;
+        a.sc.cflag[li] = live ? pl.wovf : 0;
+        a.sc.crej[li] = (live && th > KEY_NEG_INF) ? th - 1u : 0u;
+        __hip_atomic_fetch_add(&a.sc.done[row], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        pl.ncand = 0;
+        pl.wovf = 0;
+    }
+}
+
+// Finish row r: gather its PARTS partial results and decide (all threads).
+__device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t *dyn, PipeLds &pl, int slot) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const RowState &st = a.st;
+    const Scratch &sc = a.sc;
+    const qs_row_param P = st.prm[row];
+    if (tid == 0) {
+        int it = 0;
+        while (__hip_atomic_load(&sc.done[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < PARTS) {
+            if (++it >= SPIN_LIMIT) {
+                atomicOr(sc.err, 4);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    const int l0 = row * PARTS;
+    if (tid < 64) {
+        const bool have = lane < PARTS;
+        if (row_greedy(P)) {
+            float bv = have ? sc.bestv[l0 + lane] : -INFINITY;
+            int bi = have ? sc.besti[l0 + lane] : -1;
+            const float mx = wave_max_f(bv);
+            wave_best(bv, bi);
+            if (lane == 0) { pl.gbv = bv; pl.gbi = bi; pl.tot.maxl = mx; }
+        } else {
+            double ps = have ? sc.psum[l0 + lane] : 0.0;
+            int pc = have ? sc.pcnt[l0 + lane] : 0;
+            int cc = have ? sc.ccnt[l0 + lane] : 0;
+            int cf = have ? sc.cflag[l0 + lane] : 0;
+            uint32_t cr = have ? sc.crej[l0 + lane] : 0u;
+            ps = wave_sum_d(ps);
+            pc = wave_sum_i(pc);
+            cf = wave_or_i(cf);
+            cr = wave_max_u(cr);
+            int incl = cc;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            if (have) pl.offs[lane] = incl - cc;
+            if (lane == 63) pl.offs[PARTS] = incl;
+            if (lane == 0) {
+                pl.tot.maxl = key2f(__hip_atomic_load(&sc.rowmax[row], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+                pl.tot.sum = ps;
+                pl.tot.nwin = pc;
+                pl.tot.cflag = cf;
+                pl.tot.rej = cr;
+            }
+        }
+    }
+    __syncthreads();
+    const float *x = a.logits + (int64_t)row * a.stride;
+    if (row_greedy(P)) {
+        if (tid == 0) record_greedy(row, P, pl.gbv, pl.gbi, pl.tot.maxl, x[0], st, a.out, a.diag);
+    } else {
+        uint32_t *keys = dyn;
+        int32_t *ids = (int32_t *)(dyn + FCAP);
+        uint64_t *srt = (uint64_t *)(dyn + 2 * FCAP);
+        FullLds<NT> &fl = *(FullLds<NT> *)dyn;       // aliases keys/ids (dead by then)
+        RowTotals t = pl.tot;
+        t.total = pl.offs[PARTS];
+        if (t.total <= FCAP && isfinite(t.maxl * P.inv_t)) {
+            for (int j = tid; j < t.total; j += NT) {
+                int p = 0;
+                while (j >= pl.offs[p + 1]) ++p;
+                const int64_t src = (int64_t)(l0 + p) * PCAP + (j - pl.offs[p]);
+                keys[j] = sc.ckey[src];
+                ids[j] = sc.cid[src];
+            }
+        }
+        __syncthreads();
+        decide_row<NT>(row, P, t, FCAP, keys, ids, srt, pl.dl, fl, x, a.vocab, st, sc, a.out,
+                       a.diag, slot);
+    }
+    __syncthreads();
+    if (tid == 0) {                               // ready for the next pick
+        sc.arrive[row] = 0;
+        sc.done[row] = 0;
+        sc.rowmax[row] = 0u;
+    }
+}
+
+// One stage: `cur` holds the completed part s, `nxt` the completed part s+1, `ld` is
+// loading part s+2 (and receives part s+3 once `cur` is free: the caller rotates roles).
+__device__ __forceinline__ void stage(float4 (&cur)[UP], float4 (&ld)[UP], int s,
+                                      const PipeArgs &a, const Geo &g, int w, uint32_t *bm,
+                                      uint32_t *ckey, int32_t *cid, uint32_t *tm0,
+                                      uint32_t *tm1, PipeLds &pl) {
+    const int tid = threadIdx.x;
+    const bool data = tid >= 64;
+    const bool v0 = task_valid(a, s, g, w), v1 = task_valid(a, s + 1, g, w),
+               v2 = task_valid(a, s + 2, g, w), v3 = task_valid(a, s + 3, g, w);
+    const int r0 = task_row(s, w, g.rps), r1 = task_row(s + 1, w, g.rps),
+              r2 = task_row(s + 2, w, g.rps), r3 = task_row(s + 3, w, g.rps);
+    __syncthreads();
+    if (data) {
+        if (v0) sum_part(cur, a, r0, g, ckey, cid, pl.maxkey[s & 1], pl.theta[s & 1], pl);
+    } else {
+        RingIds ring2;                           // in flight while publishing and polling
+        if (v2) ring2 = ring_fetch(a, r2);
+        if (v1) {
+            control_publish(a, r1, g, pl);       // part s+1 was completed last stage
+            if (!row_greedy(a.st.prm[r1])) {
+                const uint32_t key = poll_rowmax(a, r1);
+                const qs_row_param P1 = a.st.prm[r1];
+                const uint32_t th = wave_kth16_lds((s + 1) & 1 ? tm1 : tm0, DT,
+                                                 min(2 * row_ksel(P1), DT));
+                if ((tid & 63) == 0) {
+                    pl.maxkey[(s + 1) & 1] = key;
+                    pl.theta[(s + 1) & 1] = th;
+                }
+            }
+        }
+        if (v2) bitmap_build(bm, ring2, a, r2, g);
+    }
+    __syncthreads();
+    if (data) {
+        if (v2) complete_part(ld, a, r2, g, bm, (s & 1) ? tm1 : tm0, pl);
+        if (v3) issue_loads(cur, a, r3, g);
+    } else if (v0) {
+        control_store(a, r0, g, pl.maxkey[s & 1], pl.theta[s & 1], ckey, cid, pl);
+    }
+}
+
+__global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
+    extern __shared__ uint32_t dyn[];
+    __shared__ PipeLds pl;
+    const int w = blockIdx.x, tid = threadIdx.x;
+    const bool data = tid >= 64;
+    Geo g;
+    g.rps = gridDim.x / PARTS;
+    g.part = w / g.rps;
+    g.lo = g.part * a.part_len;
+    const int p_hi = min(g.lo + a.part_len, a.vocab);
+    g.c_lo = g.lo >> 2;
+    g.c_hi = p_hi >> 2;
+    g.bm_words = a.part_len / 32 + 1;
+    uint32_t *bm = dyn;
+    uint32_t *ckey = dyn + g.bm_words;
+    int32_t *cid = (int32_t *)(ckey + PCAP);
+    uint32_t *tm0 = (uint32_t *)(cid + PCAP);
+    uint32_t *tm1 = tm0 + DT;
+    if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];
+    if (tid == 0) { pl.ncand = 0; pl.wovf = 0; }
+
+    float4 B0[UP], B1[UP], B2[UP];
+    // prologue: parts 0 and 1 completed and part 0's max known; part 2 loading
+    const bool t0 = task_valid(a, 0, g, w), t1 = task_valid(a, 1, g, w),
+               t2 = task_valid(a, 2, g, w);
+    const int r0 = task_row(0, w, g.rps), r1 = task_row(1, w, g.rps), r2 = task_row(2, w, g.rps);
+    if (data) {
+        if (t0) issue_loads(B0, a, r0, g);
+        if (t1) issue_loads(B1, a, r1, g);
+    } else if (t0) {
+        control_bitmap(bm, a, r0, g);
+    }
+    __syncthreads();
+    if (data && t0) complete_part(B0, a, r0, g, bm, tm0, pl);
+    __syncthreads();
+    if (data) {
+        if (t2) issue_loads(B2, a, r2, g);
+    } else if (t0) {
+        control_publish(a, r0, g, pl);
+        if (t1) control_bitmap(bm, a, r1, g);
+    }
+    __syncthreads();
+    if (data) {
+        if (t1) complete_part(B1, a, r1, g, bm, tm1, pl);
+    } else if (t0 && !row_greedy(a.st.prm[r0])) {
+        const uint32_t key = poll_rowmax(a, r0);
+        const uint32_t th = wave_kth16_lds(tm0, DT, min(2 * row_ksel(a.st.prm[r0]), DT));
+        if ((tid & 63) == 0) {
+            pl.maxkey[0] = key;
+            pl.theta[0] = th;
+        }
+    }
+    // stages: buffer roles rotate with period 3
+    for (int s = 0; s < a.stages; s += 3) {
+        stage(B0, B2, s, a, g, w, bm, ckey, cid, tm0, tm1, pl);
+        if (s + 1 >= a.stages) break;
+        stage(B1, B0, s + 1, a, g, w, bm, ckey, cid, tm0, tm1, pl);
+        if (s + 2 >= a.stages) break;
+        stage(B2, B1, s + 2, a, g, w, bm, ckey, cid, tm0, tm1, pl);
+    }
+    __syncthreads();
+    // epilogue: rows r = w (mod G), each with this workgroup's full-window slot
+    for (int r = w; r < a.n_rows; r += gridDim.x) finish_row(a, r, dyn, pl, w);
+}
+
+}  // namespace
+
+int qs_pipe_supported(int n_rows, int n_vocab, int64_t row_stride, const void *logits,
+                      int grid) {
+    if (grid < 64 || grid % 64 != 0) return 0;
+    if (n_vocab % 4 != 0 || row_stride % 4 != 0 || ((uintptr_t)logits % 16) != 0) return 0;
+    const int part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
+    if (part_len > 4 * DT * UP || part_len < 4 * DT * (UP - 1)) return 0;
+    if ((int64_t)n_rows * PARTS < grid) return 0;     // too few rows to fill the grid
+    return 1;
+}
+
+size_t qs_pipe_lds_bytes(int n_vocab) {
+    const int part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
+    const size_t pipe = sizeof(uint32_t) * ((size_t)part_len / 32 + 1 + 2 * PCAP + 2 * DT);
+    const size_t epi = sizeof(uint32_t) * 2 * FCAP + sizeof(uint64_t) * SORT_CAP;
+    const size_t fl = sizeof(FullLds<NT>);
+    size_t m = pipe > epi ? pipe : epi;
+    return m > fl ? m : fl;
+}
+
+int qs_pipe_parts(void) { return PARTS; }
+
+int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vocab,
+                   const RowState &st, const Scratch &sc, int32_t *out, qs_pick_diag *diag,
+                   int grid, hipStream_t stream) {
+    PipeArgs a;
+    a.logits = logits;
+    a.stride = row_stride;
+    a.vocab = n_vocab;
+    a.n_rows = n_rows;
+    a.part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
+    const int rps = grid / PARTS;
+    a.stages = (n_rows + rps - 1) / rps;
+    a.st = st;
+    a.sc = sc;
+    a.out = out;
+    a.diag = diag;
+    void *args[] = {&a};
+    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_pipe, dim3(grid), dim3(NT),
+                                                    args, qs_pipe_lds_bytes(n_vocab), stream);
+    if (e != hipSuccess) {
+        qs_set_error("k_pipe cooperative launch: %s", hipGetErrorString(e));
+        return e == hipErrorOutOfMemory ? QS_ENOMEM : QS_EDEVICE;
+    }
+    return 0;
+}
