@@ -40,7 +40,7 @@ def parse():
                     help="approximate CPU work for the baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: all host cores (<= 16)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["auto", "split", "pipelined"], default="auto",
+    ap.add_argument("--mode", choices=["auto", "split", "pipelined", "onepass", "queue"], default="auto",
                     help="which kernels a pick uses (qs_batch_set_mode)")
     return ap.parse_args()
 
@@ -101,7 +101,8 @@ def main():
     hist = orc.gen_hist(w.seed, 0, B, w.hist_len, V, w.hist_pool) if w.hist_len else None
     batch = qa.Batch(B, V, max(1, w.repeat_last_n))
     batch.set_mode({"auto": qa.MODE_AUTO, "split": qa.MODE_SPLIT,
-                    "pipelined": qa.MODE_PIPELINED}[args.mode])
+                    "pipelined": qa.MODE_PIPELINED, "onepass": qa.MODE_ONEPASS,
+                    "queue": qa.MODE_QUEUE}[args.mode])
     batch.config(0, B, *w.params(), seeds=seeds)
     if hist is not None:
         batch.set_history(0, hist)
@@ -150,8 +151,10 @@ def main():
                    "mode": args.mode, "description": w.description},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": ("one pick (k_pipe)" if args.mode == "pipelined" else
-                                "one pick (k_scan + k_expsum + k_finalize)"),
+                     "kernel": {"pipelined": "one pick (k_pipe)",
+                                "onepass": "one pick (k_onepass)",
+                                "queue": "one pick (k_queue)"}.get(
+                                    args.mode, "one pick (k_scan + k_expsum + k_finalize)"),
                      "bytes_per_step": alg_bytes},
         "cpu_baseline": cpu,
         "parity": parity,

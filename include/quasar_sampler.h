@@ -123,12 +123,15 @@ int qs_batch_set_history(qs_batch *b, int row0, int n_rows, const int32_t *ids,
 int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
                   int n_vocab, int32_t *d_out, qs_pick_diag *d_diag);
 
-/* Which kernels qs_batch_pick uses.  AUTO (the default) takes the split-row kernels,
- * currently the faster path at every measured batch size.  PIPELINED takes the
- * persistent pipelined kernel (at least one row per 4 CUs, vocabulary a multiple of 4 up
- * to 153,600, 16-byte aligned rows) and returns QS_EINVAL on a pick it does not support.
- * The results are identical; the modes exist for testing and measurement. */
-enum { QS_MODE_AUTO = 0, QS_MODE_SPLIT = 1, QS_MODE_PIPELINED = 2 };
+/* Which kernels qs_batch_pick uses.  AUTO (the default) takes the split-row kernels.
+ * SPLIT: three kernels per pick, the logits streamed twice.  PIPELINED: the persistent
+ * pipelined kernel (at least one row per 4 CUs, vocabulary a multiple of 4 up to
+ * 153,600, 16-byte aligned rows).  ONEPASS: the one-pass kernel, every logit read once
+ * (vocabularies up to 655,360).  QUEUE: one persistent kernel over a queue of scan and
+ * sum tasks (vocabularies up to 655,360).  A mode that does not support a pick returns
+ * QS_EINVAL.  The results are identical; the modes exist for testing and measurement. */
+enum { QS_MODE_AUTO = 0, QS_MODE_SPLIT = 1, QS_MODE_PIPELINED = 2, QS_MODE_ONEPASS = 3,
+       QS_MODE_QUEUE = 4 };
 int qs_batch_set_mode(qs_batch *b, int mode);
 
 /* Set one row's generator state and history exactly (oldest first), e.g. to carry a

@@ -17,12 +17,13 @@ import ctypes as C
 import numpy as np
 
 from . import _native
-from ._native import (MODE_AUTO, MODE_PIPELINED, MODE_SPLIT, PATH_EMPTY, PATH_FAST,
-                      PATH_FULL, PATH_GREEDY, PickDiag, QsError, check, load)
+from ._native import (MODE_AUTO, MODE_ONEPASS, MODE_PIPELINED, MODE_QUEUE, MODE_SPLIT,
+                      PATH_EMPTY, PATH_FAST, PATH_FULL, PATH_GREEDY, PickDiag, QsError, check,
+                      load)
 
 __all__ = ["Sampler", "Batch", "DeviceBuffer", "gen_logits_device", "device_info",
            "PickDiag", "QsError", "PATH_GREEDY", "PATH_FAST", "PATH_FULL", "PATH_EMPTY",
-           "MODE_AUTO", "MODE_SPLIT", "MODE_PIPELINED"]
+           "MODE_AUTO", "MODE_SPLIT", "MODE_PIPELINED", "MODE_ONEPASS", "MODE_QUEUE"]
 
 
 class DeviceBuffer:
@@ -142,7 +143,8 @@ class Batch:
         check(self._lib.qs_batch_reset(self._b, row0, n_rows), "qs_batch_reset")
 
     def set_mode(self, mode):
-        """0: automatic, 1: split-row kernels, 2: pipelined kernel (see quasar_sampler.h)."""
+        """0: automatic, 1: split-row kernels, 2: pipelined kernel, 3: one-pass kernel,
+        4: queue kernel (see quasar_sampler.h)."""
         check(self._lib.qs_batch_set_mode(self._b, int(mode)), "qs_batch_set_mode")
 
     def set_history(self, row0, ids):

@@ -12,7 +12,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libquasar_sampler.so")
 
 QS_EINVAL, QS_ENOMEM, QS_EDEVICE = -22, -12, -5
 PATH_GREEDY, PATH_FAST, PATH_FULL, PATH_EMPTY = 0, 1, 2, 3
-MODE_AUTO, MODE_SPLIT, MODE_PIPELINED = 0, 1, 2
+MODE_AUTO, MODE_SPLIT, MODE_PIPELINED, MODE_ONEPASS, MODE_QUEUE = 0, 1, 2, 3, 4
 
 
 class PickDiag(C.Structure):

@@ -437,6 +437,10 @@ struct qs_batch {
     int max_rows = 0, max_vocab = 0, max_last_n = 0;
     int mode = QS_MODE_AUTO;               // QS_MODE_*: which kernels a pick uses
     int pipe_grid = 0;                     // persistent workgroups of the pipelined kernel
+    int op_grid = 0;                       // resident workgroups of the one-pass kernel
+    int q_grid = 0;                        // resident workgroups of the queue kernel
+    int q_lag = 0;                         // queue: rows of scans ahead of the sums (0: auto)
+    OpScratch op{};
     int slice_rows = 0;                    // capacity of the per-slice scratch (rows*S)
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -454,7 +458,8 @@ static void batch_release(qs_batch *b) {
                     b->sc.bestv, b->sc.besti, b->sc.sth, b->sc.ckey, b->sc.cid, b->sc.ccnt,
                     b->sc.crej, b->sc.cflag, b->sc.psum, b->sc.pcnt, b->sc.locks,
                     b->sc.full_keys, b->sc.full_bm, b->sc.err, b->sc.rowmax, b->sc.arrive,
-                    b->sc.done};
+                    b->sc.done, b->op.ctl, b->op.ctr, b->op.psum, b->op.pcnt, b->op.rej, b->op.ccnt,
+                    b->op.ckey, b->op.cid, b->op.bestv, b->op.besti};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     if (b->ev0) (void)hipEventDestroy(b->ev0);
@@ -479,6 +484,12 @@ static int batch_alloc(qs_batch *b) {
         return QS_EDEVICE;
     }
     b->pipe_grid = coop ? ncu / qs_pipe_parts() * qs_pipe_parts() : 0;
+    b->op_grid = qs_onepass_grid();
+    b->q_grid = qs_queue_grid();
+    if (const char *e = getenv("QS_QUEUE_LAG_ROWS")) b->q_lag = atoi(e);
+    int oc = qs_onepass_slice_cap(R, V);
+    if (qs_queue_slice_cap(R, V) > oc) oc = qs_queue_slice_cap(R, V);
+    b->op.slice_cap = oc;
     int slots = R < SLOTS ? R : SLOTS;
     if (b->pipe_grid > 0 && R > slots) slots = R < b->pipe_grid ? R : b->pipe_grid;
     b->sc.nslots = slots;
@@ -507,6 +518,19 @@ static int batch_alloc(qs_batch *b) {
     if (!rc) rc = dev_alloc(&b->sc.rowmax, R, "rowmax");
     if (!rc) rc = dev_alloc(&b->sc.arrive, R, "arrive");
     if (!rc) rc = dev_alloc(&b->sc.done, R, "done");
+    if (!rc) rc = dev_alloc(&b->op.ctl, 2, "queue tickets");
+    if (!rc) rc = dev_alloc(&b->op.ctr, (size_t)R * QS_OP_CTR_STRIDE, "op counters");
+    if (!rc) rc = dev_alloc(&b->op.psum, oc, "op psum");
+    if (!rc) rc = dev_alloc(&b->op.pcnt, oc, "op pcnt");
+    if (!rc) rc = dev_alloc(&b->op.rej, oc, "op rej");
+    if (!rc) rc = dev_alloc(&b->op.ccnt, oc, "op ccnt");
+    if (!rc) rc = dev_alloc(&b->op.ckey, (size_t)oc * QS_OP_CPS, "op ckey");
+    if (!rc) rc = dev_alloc(&b->op.cid, (size_t)oc * QS_OP_CPS, "op cid");
+    if (!rc) rc = dev_alloc(&b->op.bestv, oc, "op bestv");
+    if (!rc) rc = dev_alloc(&b->op.besti, oc, "op besti");
+    if (!rc && hipMemset(b->op.ctr, 0, sizeof(uint32_t) * R * QS_OP_CTR_STRIDE) != hipSuccess)
+        rc = QS_EDEVICE;
+    if (!rc && hipMemset(b->op.ctl, 0, sizeof(int32_t) * 2) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * R) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.arrive, 0, sizeof(int32_t) * R) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.done, 0, sizeof(int32_t) * R) != hipSuccess) rc = QS_EDEVICE;
@@ -692,6 +716,23 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
         qs_set_error("qs_batch_pick: the pipelined kernel does not support this pick");
         return QS_EINVAL;
     }
+    const bool op_ok = b->op_grid > 0 && kmax <= K_MAX && n_vocab <= b->max_vocab;
+    if (b->mode == QS_MODE_QUEUE) {
+        if (b->q_grid <= 0 || kmax > K_MAX) {
+            qs_set_error("qs_batch_pick: the queue kernel does not support this pick");
+            return QS_EINVAL;
+        }
+        return qs_queue_launch(d_logits, row_stride, n_rows, n_vocab, kmax, st0, b->sc, b->op,
+                               d_out, d_diag, b->q_grid, b->q_lag, b->stream);
+    }
+    if (b->mode == QS_MODE_ONEPASS) {
+        if (!op_ok) {
+            qs_set_error("qs_batch_pick: the one-pass kernel does not support this pick");
+            return QS_EINVAL;
+        }
+        return qs_onepass_launch(d_logits, row_stride, n_rows, n_vocab, kmax, st0, b->sc, b->op,
+                                 d_out, d_diag, b->op_grid, b->stream);
+    }
     if (b->mode == QS_MODE_PIPELINED) {
         return qs_pipe_launch(d_logits, row_stride, n_rows, n_vocab, st0, b->sc, d_out, d_diag,
                               b->pipe_grid, b->stream);
@@ -734,7 +775,7 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
 }
 
 int qs_batch_set_mode(qs_batch *b, int mode) {
-    if (!b || mode < QS_MODE_AUTO || mode > QS_MODE_PIPELINED) {
+    if (!b || mode < QS_MODE_AUTO || mode > QS_MODE_QUEUE) {
         qs_set_error("qs_batch_set_mode: bad mode %d", mode);
         return QS_EINVAL;
     }
@@ -754,6 +795,8 @@ int qs_batch_synchronize(qs_batch *b) {
         (void)hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * b->max_rows);
         (void)hipMemset(b->sc.arrive, 0, sizeof(int32_t) * b->max_rows);
         (void)hipMemset(b->sc.done, 0, sizeof(int32_t) * b->max_rows);
+        (void)hipMemset(b->op.ctr, 0, sizeof(uint32_t) * b->max_rows * QS_OP_CTR_STRIDE);
+        (void)hipMemset(b->op.ctl, 0, sizeof(int32_t) * 2);
         qs_set_error("a bounded wait on the device gave up (flags %d); the rows involved "
                      "returned wrong ids", err);
         return QS_EDEVICE;

@@ -80,6 +80,27 @@ __device__ __forceinline__ void wave_best(float &v, int &i) {
     }
 }
 
+// ---- data shared between workgroups of one launch ----------------------------------------
+//
+// Loads and stores at device scope (sc1: coherent across the XCDs' L2 caches), ordered by
+// waiting for the stores to complete before the relaxed counter update that announces
+// them.  No L2 writeback or invalidation is issued, so the streaming loads of the other
+// workgroups keep their cache lines.
+template <typename T>
+__device__ __forceinline__ void st_dev(T *p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ld_dev(const T *p) {
+    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every vector memory operation of the calling wavefront has completed.
+__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+template <typename T>
+__device__ __forceinline__ T add_dev(T *p, T v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- the reference's scalar steps ----------------------------------------------------------
 
 // sample.c:124: a history logit is divided by the penalty when positive, multiplied
@@ -571,9 +592,9 @@ struct DecideLds {
 // sample.c:136-178 for a sampling row whose candidates (keys[0..t.total), ids) are in LDS:
 // radix-select the top K by logit, exact p, bitonic sort, prove the prefix, decide and
 // record; rows the proof does not cover go through full_row.  fcap bounds t.total,
-// srt holds SORT_CAP keys.  fixed_slot >= 0 names a full-window scratch slot owned by the
+// srt holds SC keys.  fixed_slot >= 0 names a full-window scratch slot owned by the
 // caller, -1 takes one under the slot locks.  All threads of the block call this.
-template <int NT>
+template <int NT, int SC = SORT_CAP>
 __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const RowTotals &t, int fcap,
                            uint32_t *keys, int32_t *ids, uint64_t *srt, DecideLds<NT> &dl,
                            FullLds<NT> &fl, const float *x, int V, const RowState &st,
@@ -630,7 +651,7 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
             wbase = __shfl(wbase, 0, 64);
             if (keep) {
                 const int pos = wbase + lane_prefix(m);
-                if (pos < SORT_CAP) {
+                if (pos < SC) {
                     const float s = key2f(k) * inv_t;
                     uint64_t key = 0ull;               // out of the window: sorts last
                     if (s >= thr) key = pid_key(qs_expf_core(s - msc, tab) * inv, ids[j]);
@@ -643,7 +664,7 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
         __syncthreads();
         nkept = dl.sh[3];
         rej = dl.shu[0];
-        if (nkept > SORT_CAP) full = true;
+        if (nkept > SC) full = true;
     }
     if (!full) {
         int npad = 1;

@@ -231,16 +231,14 @@ __device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row) {
     uint32_t key = 0u;
     if (lane == 0) {
         int it = 0;
-        while (__hip_atomic_load(&a.sc.arrive[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-               PARTS) {
+        while (ld_dev(&a.sc.arrive[row]) < PARTS) {
             if (++it >= SPIN_LIMIT) {
                 atomicOr(a.sc.err, 2);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        key = __hip_atomic_load(&a.sc.rowmax[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        key = ld_dev(&a.sc.rowmax[row]);
     }
     return __shfl(key, 0, 64);
 }
@@ -332,15 +330,17 @@ __device__ __forceinline__ void control_publish(const PipeArgs &a, int row, cons
         float v0 = pl.wbv[1];
         int i0 = pl.wbi[1];
         for (int k = 2; k < NWV; ++k) best_combine(v0, i0, pl.wbv[k], pl.wbi[k]);
-        a.sc.bestv[li] = v0;
-        a.sc.besti[li] = i0;
-        __hip_atomic_fetch_add(&a.sc.done[row], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        st_dev(&a.sc.bestv[li], v0);
+        st_dev(&a.sc.besti[li], i0);
+        stores_done();
+        add_dev(&a.sc.done[row], 1);
         return;
     }
     float t = pl.wmax[1];
     for (int k = 2; k < NWV; ++k) t = fmaxf(t, pl.wmax[k]);
     __hip_atomic_fetch_max(&a.sc.rowmax[row], f2key(t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(&a.sc.arrive[row], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    stores_done();
+    add_dev(&a.sc.arrive[row], 1);
 }
 
 // Control wave: store a summed part's results and release them.
@@ -357,8 +357,8 @@ __device__ __forceinline__ void control_store(const PipeArgs &a, int row, const 
     uint32_t *gk = a.sc.ckey + (int64_t)li * PCAP;
     int32_t *gi = a.sc.cid + (int64_t)li * PCAP;
     for (int j = lane; j < n; j += 64) {
-        gk[j] = ckey[j];
-        gi[j] = cid[j];
+        st_dev(&gk[j], ckey[j]);
+        st_dev(&gi[j], cid[j]);
     }
     if (lane == 0) {
         double t = 0.0;
@@ -368,12 +368,15 @@ __device__ __forceinline__ void control_store(const PipeArgs &a, int row, const 
                 t += pl.wsum[k];
                 ct += pl.wcnt[k];
             }
-        a.sc.psum[li] = t;
-        a.sc.pcnt[li] = ct;
-        a.sc.ccnt[li] = n;
-        a.sc.cflag[li] = live ? pl.wovf : 0;
-        a.sc.crej[li] = (live && th > KEY_NEG_INF) ? th - 1u : 0u;
-        __hip_atomic_fetch_add(&a.sc.done[row], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        st_dev(&a.sc.psum[li], t);
+        st_dev(&a.sc.pcnt[li], ct);
+        st_dev(&a.sc.ccnt[li], n);
+        st_dev(&a.sc.cflag[li], live ? pl.wovf : 0);
+        st_dev(&a.sc.crej[li], (live && th > KEY_NEG_INF) ? th - 1u : 0u);
+    }
+    stores_done();                                // the whole wave's stores, then the count
+    if (lane == 0) {
+        add_dev(&a.sc.done[row], 1);
         pl.ncand = 0;
         pl.wovf = 0;
     }
@@ -387,31 +390,30 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
     const qs_row_param P = st.prm[row];
     if (tid == 0) {
         int it = 0;
-        while (__hip_atomic_load(&sc.done[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < PARTS) {
+        while (ld_dev(&sc.done[row]) < PARTS) {
             if (++it >= SPIN_LIMIT) {
                 atomicOr(sc.err, 4);
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     const int l0 = row * PARTS;
     if (tid < 64) {
         const bool have = lane < PARTS;
         if (row_greedy(P)) {
-            float bv = have ? sc.bestv[l0 + lane] : -INFINITY;
-            int bi = have ? sc.besti[l0 + lane] : -1;
+            float bv = have ? ld_dev(&sc.bestv[l0 + lane]) : -INFINITY;
+            int bi = have ? ld_dev(&sc.besti[l0 + lane]) : -1;
             const float mx = wave_max_f(bv);
             wave_best(bv, bi);
             if (lane == 0) { pl.gbv = bv; pl.gbi = bi; pl.tot.maxl = mx; }
         } else {
-            double ps = have ? sc.psum[l0 + lane] : 0.0;
-            int pc = have ? sc.pcnt[l0 + lane] : 0;
-            int cc = have ? sc.ccnt[l0 + lane] : 0;
-            int cf = have ? sc.cflag[l0 + lane] : 0;
-            uint32_t cr = have ? sc.crej[l0 + lane] : 0u;
+            double ps = have ? ld_dev(&sc.psum[l0 + lane]) : 0.0;
+            int pc = have ? ld_dev(&sc.pcnt[l0 + lane]) : 0;
+            int cc = have ? ld_dev(&sc.ccnt[l0 + lane]) : 0;
+            int cf = have ? ld_dev(&sc.cflag[l0 + lane]) : 0;
+            uint32_t cr = have ? ld_dev(&sc.crej[l0 + lane]) : 0u;
             ps = wave_sum_d(ps);
             pc = wave_sum_i(pc);
             cf = wave_or_i(cf);
@@ -424,8 +426,7 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
             if (have) pl.offs[lane] = incl - cc;
             if (lane == 63) pl.offs[PARTS] = incl;
             if (lane == 0) {
-                pl.tot.maxl = key2f(__hip_atomic_load(&sc.rowmax[row], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT));
+                pl.tot.maxl = key2f(ld_dev(&sc.rowmax[row]));
                 pl.tot.sum = ps;
                 pl.tot.nwin = pc;
                 pl.tot.cflag = cf;
@@ -449,8 +450,8 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
                 int p = 0;
                 while (j >= pl.offs[p + 1]) ++p;
                 const int64_t src = (int64_t)(l0 + p) * PCAP + (j - pl.offs[p]);
-                keys[j] = sc.ckey[src];
-                ids[j] = sc.cid[src];
+                keys[j] = ld_dev(&sc.ckey[src]);
+                ids[j] = ld_dev(&sc.cid[src]);
             }
         }
         __syncthreads();
@@ -459,9 +460,9 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
     }
     __syncthreads();
     if (tid == 0) {                               // ready for the next pick
-        sc.arrive[row] = 0;
-        sc.done[row] = 0;
-        sc.rowmax[row] = 0u;
+        st_dev(&sc.arrive[row], 0);
+        st_dev(&sc.done[row], 0);
+        st_dev(&sc.rowmax[row], 0u);
     }
 }
 

@@ -313,11 +313,19 @@ def _run_mode(qa, mode, w, B, picks, logits_buf, seeds, hist, per_row=None):
     return ids, paths, states
 
 
+MODES = {"pipelined": 2, "onepass": 3, "queue": 4}
+
+
+@pytest.mark.parametrize("mode", sorted(MODES))
 @pytest.mark.parametrize("name,B,picks", [("peaked_b256", 256, 3), ("large_b4096", 512, 2),
-                                          ("studentt_b1024", 1024, 1)])
-def test_pipelined_equals_split(qa, oracle, name, B, picks):
-    """The pipelined kernel and the split-row kernels return the same ids, generator
-    states and histories, pick after pick; the first pick is also checked on the CPU."""
+                                          ("studentt_b1024", 1024, 1), ("full_b1", 1, 4),
+                                          ("greedy_b1", 1, 3), ("nucleus_b8", 8, 2)])
+def test_mode_equals_split(qa, oracle, mode, name, B, picks):
+    """The pipelined and one-pass kernels return the same ids, generator states and
+    histories as the split-row kernels, pick after pick; the first pick is also checked
+    on the CPU."""
+    if mode == "pipelined" and B < 64:
+        pytest.skip("the pipelined kernel needs a batch that fills the GPU")
     w = allw()[name]
     V = w.vocab
     buf = qa.DeviceBuffer(4 * B * V)
@@ -325,26 +333,27 @@ def test_pipelined_equals_split(qa, oracle, name, B, picks):
     seeds = oracle.gen_row_seeds(w.seed, 0, B)
     hist = oracle.gen_hist(w.seed, 0, B, w.hist_len, V, w.hist_pool) if w.hist_len else None
     sp_ids, sp_paths, sp_states = _run_mode(qa, qa.MODE_SPLIT, w, B, picks, buf, seeds, hist)
-    pp_ids, pp_paths, pp_states = _run_mode(qa, qa.MODE_PIPELINED, w, B, picks, buf, seeds, hist)
+    pp_ids, pp_paths, pp_states = _run_mode(qa, MODES[mode], w, B, picks, buf, seeds, hist)
     for k in range(picks):
         assert (sp_ids[k] == pp_ids[k]).all(), (k, np.nonzero(sp_ids[k] != pp_ids[k])[0][:10])
     for r in range(B):
         assert sp_states[r][0] == pp_states[r][0] and (sp_states[r][1] == pp_states[r][1]).all()
-    for r in list(range(8)) + [B - 1]:
+    for r in sorted(set(list(range(min(B, 8))) + [B - 1])):
         x = buf.download(np.float32, V, offset=4 * r * V)
         s = oracle.sampler()
         s.config(*w.params(), seed=int(seeds[r]))
         if hist is not None:
             s.set_history(hist[r])
         assert s.pick(x) == int(pp_ids[0][r]), r
-    log(f"{name} B={B}: pipelined == split over {picks} picks; paths {set(sum(pp_paths, []))}")
+    log(f"{name} B={B}: {mode} == split over {picks} picks; paths {set(sum(pp_paths, []))}")
     buf.free()
 
 
-def test_pipelined_mixed_rows(qa, oracle):
+@pytest.mark.parametrize("mode", sorted(MODES))
+def test_mode_mixed_rows(qa, oracle, mode):
     """A 64-row batch at the full vocabulary where each row has its own parameters
-    (greedy rows, top-k off, penalties, degenerate rows), through the pipelined kernel,
-    against the CPU restatement row by row over three picks."""
+    (greedy rows, top-k off, penalties, degenerate rows), through the pipelined or the
+    one-pass kernel, against the CPU restatement row by row over three picks."""
     rng = np.random.default_rng(21)
     B, V = 64, 151936
     x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
@@ -362,7 +371,7 @@ def test_pipelined_mixed_rows(qa, oracle):
         per_row.append((cfg, int(rng.integers(1, 2**62))))
         hists.append(rng.integers(0, V, 32).astype(np.int32))
     b = qa.Batch(B, V, 64)
-    b.set_mode(qa.MODE_PIPELINED)
+    b.set_mode(MODES[mode])
     for r, (cfg, seed) in enumerate(per_row):
         b.config(r, 1, *cfg, seeds=[seed])
         b.set_history(r, hists[r])
@@ -378,3 +387,56 @@ def test_pipelined_mixed_rows(qa, oracle):
         assert rs == s.rng and (h == s.history()).all(), r
     b.close()
     buf.free()
+
+
+@pytest.mark.parametrize("mode", ["onepass", "queue"])
+def test_history_layouts(qa, oracle, mode):
+    """Histories the one-pass and queue kernels set aside in unusual shapes: runs of
+    consecutive ids (several in one thread's registers), duplicates, ids at slice edges
+    and the row's argmax itself, unaligned rows (scalar loads) and short odd
+    vocabularies."""
+    rng = np.random.default_rng(33)
+    for V, stride, aligned in [(151936, 151936, True), (151933, 151937, False),
+                               (1000, 1001, False), (4099, 4100, True)]:
+        B = 12
+        x = np.full((B, stride), np.float32(np.nan), dtype=np.float32)
+        x[:, :V] = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+        hists = []
+        for r in range(B):
+            top = int(np.argmax(x[r, :V]))
+            kind = r % 4
+            if kind == 0:
+                h = np.arange(min(V, 300), dtype=np.int64) + rng.integers(0, max(1, V - 300))
+            elif kind == 1:
+                h = rng.integers(0, 64, 200)
+            elif kind == 2:
+                edges = [i for i in range(0, V, 64)][:150]
+                h = np.array(edges + [V - 1, top], dtype=np.int64)
+            else:
+                h = np.array([top] * 5 + list(rng.integers(0, V, 100)), dtype=np.int64)
+            hists.append((h % V).astype(np.int32))
+        flat = x.reshape(-1)
+        if not aligned:
+            flat = np.concatenate([np.zeros(1, np.float32), flat])
+        buf = qa.DeviceBuffer.from_array(flat)
+        base = buf.ptr + (0 if aligned else 4)
+        b = qa.Batch(B, V, 512)
+        b.set_mode(MODES[mode])
+        cfgs = []
+        for r in range(B):
+            cfg = (0.0 if r % 5 == 0 else 0.8, 0.95, 40 if r % 3 else 0, 0.05,
+                   1.3, 512)
+            cfgs.append(cfg)
+            b.config(r, 1, *cfg, seeds=[1000 + r])
+            b.set_history(r, hists[r])
+        outs = [b.pick(base, stride, B, V, diag=True) for _ in range(3)]
+        for r in range(B):
+            s = oracle.sampler()
+            s.config(*cfgs[r], seed=1000 + r)
+            s.set_history(hists[r])
+            for k in range(3):
+                want = s.pick(x[r, :V])
+                assert int(outs[k][0][r]) == want, (V, r, k, outs[k][1][r].path)
+        b.close()
+        buf.free()
+        log(f"{mode} history layouts V={V} stride={stride}: {B} rows x 3 picks match")
