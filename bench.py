@@ -7,6 +7,11 @@ region is `--steps` back-to-back picks between two HIP events on the sampler's s
 with a device synchronisation on both sides.  Generator states and histories evolve from
 step to step, as in decoding.
 
+MI355X keeps up to 256 MiB in its last-level cache (Infinity Cache), which would hold one
+batch-256 logits array whole; the picks therefore rotate over enough copies of the
+input (--buffers, default: more than 512 MiB in total) that each pick reads from HBM.
+--buffers 1 measures the warm-cache case.
+
 Also reported on the same JSON line:
   roofline      algorithmic bytes per step (4V logits + 4H history + 4 id + 16 RNG per
                 row) over the measured step time, against 8 TB/s HBM
@@ -28,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "sampled rows/s at B=256, V=151936 fp32; achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+CACHE_DEFEAT_BYTES = 512 << 20       # twice the MI355X last-level cache
 
 
 def parse():
@@ -40,6 +46,9 @@ def parse():
                     help="approximate CPU work for the baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: all host cores (<= 16)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--buffers", type=int, default=0,
+                    help="input copies the timed picks rotate over (0: enough to exceed "
+                         "twice the last-level cache)")
     ap.add_argument("--mode", choices=["auto", "split", "pipelined", "onepass", "queue"], default="auto",
                     help="which kernels a pick uses (qs_batch_set_mode)")
     return ap.parse_args()
@@ -93,8 +102,13 @@ def main():
     print(f"# device {dev_name}, {dev_mem / 2**30:.0f} GiB, {dev_cu} CUs; workload {w.name}",
           file=sys.stderr, flush=True)
 
-    logits = qa.DeviceBuffer(4 * B * V)
-    qa.gen_logits_device(logits, V, 0, B, V, w.dist, w.sigma, w.boost, w.seed)
+    nbytes = 4 * B * V
+    n_buf = args.buffers or max(1, -(-CACHE_DEFEAT_BYTES // nbytes))
+    bufs = []
+    for _ in range(n_buf):
+        bufs.append(qa.DeviceBuffer(nbytes))
+        qa.gen_logits_device(bufs[-1], V, 0, B, V, w.dist, w.sigma, w.boost, w.seed)
+    logits = bufs[0]
     from pyoracle import Oracle  # generator helpers only (seeds, history ids)
     orc = Oracle()
     seeds = orc.gen_row_seeds(w.seed, 0, B)
@@ -120,11 +134,12 @@ def main():
         parity = {"rows_checked": checked, "id_mismatches": mism}
         del host
 
-    for _ in range(args.warmup):
-        batch.pick_async(logits.ptr, V, B, V)
+    ptrs = [b.ptr for b in bufs]
+    for i in range(args.warmup):
+        batch.pick_async(ptrs[i % n_buf], V, B, V)
     qa.check(qa.load().qs_device_synchronize(), "sync")
     t0 = time.perf_counter()
-    ms = batch.time_picks(logits.ptr, V, B, V, args.steps)
+    ms = batch.time_picks(ptrs, V, B, V, args.steps)
     qa.check(qa.load().qs_device_synchronize(), "sync")
     wall = time.perf_counter() - t0
 
@@ -148,7 +163,8 @@ def main():
         "config": {"workload": w.name, "batch": B, "vocab": V, "history": w.hist_len,
                    "temperature": w.temperature, "top_k": w.top_k, "top_p": w.top_p,
                    "min_p": w.min_p, "repeat_penalty": w.repeat_penalty,
-                   "mode": args.mode, "description": w.description},
+                   "mode": args.mode, "input_buffers": n_buf,
+                   "input_bytes_total": n_buf * nbytes, "description": w.description},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "kernel": {"pipelined": "one pick (k_pipe)",

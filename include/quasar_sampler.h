@@ -175,9 +175,12 @@ int qs_gen_logits_device(float *d_out, int64_t row_stride, int64_t row0, int n_r
 int qs_expf_device(const float *d_x, float *d_y, int64_t n);
 
 /* Enqueue `iters` back-to-back qs_batch_pick calls between two HIP events recorded on the
- * batch's stream, wait, and return the elapsed milliseconds in *ms. */
-int qs_batch_time_picks(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
-                        int n_vocab, int32_t *d_out, int iters, float *ms);
+ * batch's stream, wait, and return the elapsed milliseconds in *ms.  Pick i reads
+ * d_logits[i % n_buffers]: rotating over buffers whose total exceeds the GPU's
+ * last-level cache keeps every pick's input in HBM only. */
+int qs_batch_time_picks(qs_batch *b, const float *const *d_logits, int n_buffers,
+                        int64_t row_stride, int n_rows, int n_vocab, int32_t *d_out, int iters,
+                        float *ms);
 
 #ifdef __cplusplus
 }

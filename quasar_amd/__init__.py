@@ -192,10 +192,15 @@ class Batch:
     def synchronize(self):
         check(self._lib.qs_batch_synchronize(self._b), "qs_batch_synchronize")
 
-    def time_picks(self, logits_ptr, row_stride, n_rows, n_vocab, iters):
+    def time_picks(self, logits_ptrs, row_stride, n_rows, n_vocab, iters):
+        """Time `iters` picks on the batch's stream; pick i reads logits_ptrs[i % len]
+        (a single pointer is allowed).  Returns milliseconds."""
+        if isinstance(logits_ptrs, int):
+            logits_ptrs = [logits_ptrs]
+        arr = (C.c_void_p * len(logits_ptrs))(*logits_ptrs)
         ms = C.c_float(0)
-        check(self._lib.qs_batch_time_picks(self._b, logits_ptr, row_stride, n_rows, n_vocab,
-                                            self._out.ptr, iters, C.byref(ms)),
+        check(self._lib.qs_batch_time_picks(self._b, arr, len(logits_ptrs), row_stride, n_rows,
+                                            n_vocab, self._out.ptr, iters, C.byref(ms)),
               "qs_batch_time_picks")
         return ms.value
 

@@ -52,7 +52,8 @@ PROTOS = [
     ("qs_device_synchronize", _i, []),
     ("qs_device_info", _i, [C.c_char_p, _i, C.POINTER(C.c_size_t), C.POINTER(C.c_int)]),
     ("qs_gen_logits_device", _i, [_vp, _i64, _i64, _i, _i, _i, _f, _f, _u64]),
-    ("qs_batch_time_picks", _i, [_vp, _vp, _i64, _i, _i, _vp, _i, C.POINTER(C.c_float)]),
+    ("qs_batch_time_picks", _i, [_vp, C.POINTER(_vp), _i, _i64, _i, _i, _vp, _i,
+                                 C.POINTER(C.c_float)]),
     ("qs_expf_device", _i, [_vp, _vp, _i64]),
 ]
 

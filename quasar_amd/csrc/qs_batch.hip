@@ -59,7 +59,109 @@ constexpr int FIN_CAP = 4096;        // candidates k_finalize gathers per row
 
 __constant__ uint64_t c_exp_tab[QS_EXPF_TAB_N] = QS_EXPF_TABLE_INIT;
 
+// ---- streaming helpers ---------------------------------------------------------------------
+
+// One group of U float4 per thread: float4 c = cb + u*WG + tid; logits at or past `hi`
+// read as NaN.
+template <bool VEC>
+__device__ __forceinline__ void load_group(float4 (&v)[U], const float *x, int cb, int hi) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = load4<VEC>(x, cb + u * WG + (int)threadIdx.x, hi);
+}
+
+// A group that lies wholly inside the slice: plain 16-byte loads, no tests.
+__device__ __forceinline__ void load_full(float4 (&v)[U], const float *x, int cb) {
+    const float4 *x4 = (const float4 *)x;
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = x4[cb + u * WG + (int)threadIdx.x];
+}
+
+// Stream [lo, hi) of row x through fn(group, cb) in groups of WG*U float4, in index
+// order.  With 16-byte loads (VEC: aligned rows, hi a multiple of 4) the full groups run
+// in a branch-free loop that always has the next group's loads in flight, so each wait
+// names the exact count of loads still outstanding; the partial tail group is loaded
+// with bounds tests.
+template <bool VEC, typename Fn>
+__device__ __forceinline__ void stream_slice(const float *x, int lo, int hi, Fn &&fn) {
+    constexpr int G = WG * U;
+    const int c0 = lo >> 2, c1 = (hi + 3) >> 2;
+    int cb = c0;
+    float4 va[U], vb[U];
+    if (VEC) {
+        const int nfull = (c1 - c0) / G;
+        if (nfull >= 1) {
+            load_full(va, x, cb);
+            int g = 0;
+            for (; g + 2 < nfull; g += 2) {       // va holds group g; g+1, g+2 exist
+                load_full(vb, x, cb + G);
+                fn(va, cb);
+                load_full(va, x, cb + 2 * G);
+                fn(vb, cb + G);
+                cb += 2 * G;
+            }
+            if (g + 1 < nfull) {
+                load_full(vb, x, cb + G);
+                fn(va, cb);
+                fn(vb, cb + G);
+                cb += 2 * G;
+            } else {
+                fn(va, cb);
+                cb += G;
+            }
+        }
+    }
+    for (; cb < c1; cb += G) {
+        load_group<VEC>(va, x, cb, hi);
+        fn(va, cb);
+    }
+}
+
+// History bits of the four logits starting at element i0 (LDS bitmap of [lo, hi)).
+__device__ __forceinline__ uint32_t hist_nibble(const uint32_t *bm, int i0, int lo, int hi) {
+    if (i0 >= hi) return 0u;
+    const int r = i0 - lo;
+    return (bm[r >> 5] >> (r & 31)) & 0xFu;
+}
+
+// sample.c:124 on the flagged components of one float4 (a wave-uniform skip when no lane
+// of the wavefront has a flagged component).
+__device__ __forceinline__ void penalise4(float (&w)[4], uint32_t nib, float rp) {
+    if (__ballot(nib != 0u)) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if ((nib >> k) & 1u) w[k] = penalise(w[k], rp);
+    }
+}
+
 // ---- k_scan --------------------------------------------------------------------------------
+
+// Max (greedy: first argmax) over one group of a slice.
+template <bool GREEDY>
+__device__ __forceinline__ void scan_group(const float4 (&v)[U], int cb, int lo, int hi,
+                                           const uint32_t *bm, bool pen, float rp, float &mx,
+                                           float &bv, int &bi) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i0 = (cb + u * WG + (int)threadIdx.x) << 2;
+        float w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        if (pen) penalise4(w, hist_nibble(bm, i0, lo, hi), rp);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) mx = w[k] > mx ? w[k] : mx;
+        if (GREEDY) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (w[k] > bv) { bv = w[k]; bi = i0 + k; }
+        }
+    }
+}
+
+template <bool VEC, bool GREEDY>
+__device__ __forceinline__ void scan_slice(const float *x, int lo, int hi, const uint32_t *bm,
+                                           bool pen, float rp, float &mx, float &bv, int &bi) {
+    stream_slice<VEC>(x, lo, hi, [&](const float4 (&v)[U], int cb) {
+        scan_group<GREEDY>(v, cb, lo, hi, bm, pen, rp, mx, bv, bi);
+    });
+}
 
 template <bool VEC>
 __global__ void __launch_bounds__(WG) k_scan(Geometry g, RowState st, Scratch sc) {
@@ -85,36 +187,8 @@ __global__ void __launch_bounds__(WG) k_scan(Geometry g, RowState st, Scratch sc
     float mx = -INFINITY;                 // max penalised logit of this thread
     float bv = -INFINITY;                 // greedy: best value, first index
     int bi = -1;
-    const int c0 = lo >> 2, c1 = (hi + 3) >> 2;
-    for (int cb = c0; cb < c1; cb += WG * U) {
-        float4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = load4<VEC>(x, cb + u * WG + tid, hi);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i0 = (cb + u * WG + tid) << 2;
-            float w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-            if (pen) {
-                uint32_t nib = 0u;
-                if (i0 < hi) {
-                    const int r = i0 - lo;
-                    nib = (bm[r >> 5] >> (r & 31)) & 0xFu;
-                }
-                if (__ballot(nib != 0u)) {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        if ((nib >> k) & 1u) w[k] = penalise(w[k], rp);
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) mx = w[k] > mx ? w[k] : mx;
-            if (greedy) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (w[k] > bv) { bv = w[k]; bi = i0 + k; }
-            }
-        }
-    }
+    if (greedy) scan_slice<VEC, true>(x, lo, hi, bm, pen, rp, mx, bv, bi);
+    else scan_slice<VEC, false>(x, lo, hi, bm, pen, rp, mx, bv, bi);
 
     const float m = wave_max_f(mx);
     if (lane == 0) red_f[wv] = m;
@@ -139,15 +213,80 @@ __global__ void __launch_bounds__(WG) k_scan(Geometry g, RowState st, Scratch sc
         return;
     }
     // Candidate threshold: the k-th largest thread maximum.  Those k maxima are k distinct
-    // logits of the slice, so the slice's top k all lie at or above it.
+    // logits of the slice, so the slice's top k all lie at or above it.  k is about twice
+    // the slice's share of the row's top K plus a margin: the decision proves whatever it
+    // gets, and a row whose top K crowd into one slice takes the full-window path.
     tmax[tid] = f2key(mx);
     __syncthreads();
-    const int k2 = min(2 * row_ksel(P), WG);
+    const int k2 = min(2 * ((row_ksel(P) + g.slices - 1) / g.slices) + 8, WG);
     const uint32_t th = block_kth<WG>(tmax, WG, k2, hist, sh);
     if (tid == 0) sc.sth[row * g.slices + slice] = th;
 }
 
 // ---- k_expsum ------------------------------------------------------------------------------
+
+constexpr float X_OUT = -150.0f;     // qs_expf_core of this rounds to +0
+
+struct SumState {
+    double acc0, acc1;               // partial softmax denominators (two chains)
+    int cnt;                         // window count of the wavefront (uniform)
+    int ovf;                         // candidate list overflowed
+};
+
+// Softmax numerators, window count and candidates of one group (sample.c:136-148 per
+// element).  Out-of-window lanes evaluate the exp core at X_OUT, which is exactly +0.
+__device__ __forceinline__ void sum_group(const float4 (&v)[U], int cb, int lo, int hi,
+                                          const uint32_t *bm, bool pen, float rp, float inv_t,
+                                          float msc, float thr, float thf, const uint64_t *tab,
+                                          uint32_t *ckey, int32_t *cid, int *ncand,
+                                          SumState &ss) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i0 = (cb + u * WG + (int)threadIdx.x) << 2;
+        float w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        if (pen) penalise4(w, hist_nibble(bm, i0, lo, hi), rp);
+        float s[4];
+        bool in[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s[k] = w[k] * inv_t;
+            in[k] = s[k] >= thr;
+            ss.cnt += __popcll(__ballot(in[k]));
+        }
+        if (__ballot(in[0] | in[1] | in[2] | in[3])) {
+            float e[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) e[k] = qs_expf_core(in[k] ? s[k] - msc : X_OUT, tab);
+            ss.acc0 += (double)e[0];
+            ss.acc1 += (double)e[1];
+            ss.acc0 += (double)e[2];
+            ss.acc1 += (double)e[3];
+        }
+        const float m4 = fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3]));
+        if (__ballot(m4 >= thf)) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const bool cand = w[k] >= thf;
+                const uint64_t mk = __ballot(cand);
+                if (mk) {
+                    int base = 0;
+                    if (lane == 0) base = atomicAdd(ncand, __popcll(mk));
+                    base = __shfl(base, 0, 64);
+                    if (cand) {
+                        const int pos = base + lane_prefix(mk);
+                        if (pos < CCAP) {
+                            ckey[pos] = f2key(w[k]);
+                            cid[pos] = i0 + k;
+                        } else {
+                            ss.ovf = 1;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
 
 template <bool VEC>
 __global__ void __launch_bounds__(WG) k_expsum(Geometry g, RowState st, Scratch sc) {
@@ -178,10 +317,11 @@ __global__ void __launch_bounds__(WG) k_expsum(Geometry g, RowState st, Scratch 
         }
         return;
     }
-    if (tid < QS_EXPF_TAB_N) tab[tid] = c_exp_tab[tid];
-    if (tid == 0) ncand = 0;
     const int lo = slice * g.slice_len;
     const int hi = min(lo + g.slice_len, g.vocab);
+    const float *x = g.logits + (int64_t)row * g.stride;
+    if (tid < QS_EXPF_TAB_N) tab[tid] = c_exp_tab[tid];
+    if (tid == 0) ncand = 0;
     const float rp = P.repeat_penalty;
     const bool pen = rp > 1.0f && st.hlen[row] > 0 && P.ring_cap > 0;
     uint32_t *bm = lds;
@@ -192,73 +332,13 @@ __global__ void __launch_bounds__(WG) k_expsum(Geometry g, RowState st, Scratch 
     const uint32_t th = sc.sth[li];
     const float thf = th > KEY_NEG_INF ? key2f(th) : -INFINITY;
 
-    const float *x = g.logits + (int64_t)row * g.stride;
-    double acc = 0.0;
-    int cnt = 0;
-    int ovf = 0;
-    const int c0 = lo >> 2, c1 = (hi + 3) >> 2;
-    for (int cb = c0; cb < c1; cb += WG * U) {
-        float4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = load4<VEC>(x, cb + u * WG + tid, hi);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i0 = (cb + u * WG + tid) << 2;
-            float w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-            if (pen) {
-                uint32_t nib = 0u;
-                if (i0 < hi) {
-                    const int r = i0 - lo;
-                    nib = (bm[r >> 5] >> (r & 31)) & 0xFu;
-                }
-                if (__ballot(nib != 0u)) {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        if ((nib >> k) & 1u) w[k] = penalise(w[k], rp);
-                }
-            }
-            float s[4];
-            bool in[4], cand[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                s[k] = w[k] * inv_t;
-                in[k] = s[k] >= thr;
-                cnt += in[k] ? 1 : 0;
-                cand[k] = w[k] >= thf;
-            }
-            if (__ballot(in[0] | in[1] | in[2] | in[3])) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const float e = qs_expf_core(s[k] - msc, tab);
-                    acc += in[k] ? (double)e : 0.0;
-                }
-            }
-            if (__ballot(cand[0] | cand[1] | cand[2] | cand[3])) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint64_t mk = __ballot(cand[k]);
-                    if (mk) {
-                        int base = 0;
-                        if (lane == 0) base = atomicAdd(&ncand, __popcll(mk));
-                        base = __shfl(base, 0, 64);
-                        if (cand[k]) {
-                            const int pos = base + lane_prefix(mk);
-                            if (pos < CCAP) {
-                                ckey[pos] = f2key(w[k]);
-                                cid[pos] = i0 + k;
-                            } else {
-                                ovf = 1;
-                            }
-                        }
-                    }
-                }
-            }
-        }
-    }
-    const double a = wave_sum_d(acc);
-    const int c = wave_sum_i(cnt);
-    const int o = wave_or_i(ovf);
-    if (lane == 0) { red_d[wv] = a; red_i[wv] = c | (o << 30); }
+    SumState ss{0.0, 0.0, 0, 0};
+    stream_slice<VEC>(x, lo, hi, [&](const float4 (&v)[U], int cb) {
+        sum_group(v, cb, lo, hi, bm, pen, rp, inv_t, msc, thr, thf, tab, ckey, cid, &ncand, ss);
+    });
+    const double a = wave_sum_d(ss.acc0 + ss.acc1);
+    const int o = wave_or_i(ss.ovf);
+    if (lane == 0) { red_d[wv] = a; red_i[wv] = ss.cnt | (o << 30); }
     __syncthreads();
     const int n = min(ncand, CCAP);
     uint32_t *gk = sc.ckey + (int64_t)li * sc.ccap;
@@ -360,19 +440,37 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
     RowTotals t = tot;
     t.total = offs[S];
     if (t.total <= FIN_CAP && isfinite(t.maxl * P.inv_t)) {
-        for (int s = 0; s < S; ++s) {                      // gather the slice lists
-            const int o = offs[s], c = offs[s + 1] - o;
-            const uint32_t *gk = sc.ckey + (int64_t)(l0 + s) * sc.ccap;
-            const int32_t *gi = sc.cid + (int64_t)(l0 + s) * sc.ccap;
-            for (int j = tid; j < c; j += WG) {
-                keys[o + j] = gk[j];
-                ids[o + j] = gi[j];
+        // Gather the slice lists: every load is issued before any is stored to LDS.
+        uint32_t kk[FIN_CAP / WG];
+        int32_t ii[FIN_CAP / WG];
+#pragma unroll
+        for (int q = 0; q < FIN_CAP / WG; ++q) {
+            const int j = q * WG + tid;
+            kk[q] = 0u;
+            ii[q] = 0;
+            if (j < t.total) {
+                int lo = 0, hi = S;                        // last s with offs[s] <= j
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (offs[mid] <= j) lo = mid; else hi = mid - 1;
+                }
+                const int64_t src = (int64_t)(l0 + lo) * sc.ccap + (j - offs[lo]);
+                kk[q] = sc.ckey[src];
+                ii[q] = sc.cid[src];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < FIN_CAP / WG; ++q) {
+            const int j = q * WG + tid;
+            if (j < t.total) {
+                keys[j] = kk[q];
+                ids[j] = ii[q];
             }
         }
     }
     __syncthreads();
-    decide_row<WG>(row, P, t, FIN_CAP, keys, ids, srt, dl, fl, x, g.vocab, st, sc, a.out,
-                   a.diag, -1);
+    decide_row_fast<WG>(row, P, t, FIN_CAP, keys, ids, srt, dl, fl, x, g.vocab, st, sc, a.out,
+                        a.diag, -1);
 }
 
 // ---- synthetic inputs and the expf check ---------------------------------------------------
@@ -750,7 +848,8 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
     g.bm_words = g.slice_len / 32;
     RowState st{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
                 b->max_last_n > 0 ? b->max_last_n : 1};
-    const bool vec = ((uintptr_t)d_logits % 16 == 0) && (row_stride % 4 == 0);
+    const bool vec = ((uintptr_t)d_logits % 16 == 0) && (row_stride % 4 == 0) &&
+                     (n_vocab % 4 == 0);
     const dim3 grid(g.slices, n_rows);
     const size_t lds_scan = sizeof(uint32_t) * (size_t)g.bm_words;
     const size_t lds_exp = sizeof(uint32_t) * ((size_t)g.bm_words + 2 * (size_t)CCAP);
@@ -806,12 +905,14 @@ int qs_batch_synchronize(qs_batch *b) {
 
 void *qs_batch_stream(qs_batch *b) { return b ? (void *)b->stream : nullptr; }
 
-int qs_batch_time_picks(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
-                        int n_vocab, int32_t *d_out, int iters, float *ms) {
-    if (!b || iters < 1 || !ms) return QS_EINVAL;
+int qs_batch_time_picks(qs_batch *b, const float *const *d_logits, int n_buffers,
+                        int64_t row_stride, int n_rows, int n_vocab, int32_t *d_out, int iters,
+                        float *ms) {
+    if (!b || !d_logits || n_buffers < 1 || iters < 1 || !ms) return QS_EINVAL;
     HIP_TRY(hipEventRecord(b->ev0, b->stream), "event");
     for (int i = 0; i < iters; ++i) {
-        const int rc = qs_batch_pick(b, d_logits, row_stride, n_rows, n_vocab, d_out, nullptr);
+        const int rc = qs_batch_pick(b, d_logits[i % n_buffers], row_stride, n_rows, n_vocab,
+                                     d_out, nullptr);
         if (rc) return rc;
     }
     HIP_TRY(hipEventRecord(b->ev1, b->stream), "event");

@@ -292,12 +292,16 @@ __device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)(k & 
 
 // ---- the decision over sorted candidates (one thread) --------------------------------------
 
-// sample.c:153-178 over the first positions of the (p desc, id asc) order.  srt[0..m)
-// hold in-window candidates; positions [0, E) are known to be positions of the full
-// order.  nwin is the window size.  Returns false (nothing consumed) when the cuts or the
-// draw would read a position >= E; otherwise advances rs and fills id and d.
-__device__ __forceinline__ bool decide_prefix(const uint64_t *srt, int E, int nwin, const qs_row_param &P,
-                              uint64_t &rs, int &id, qs_pick_diag &d) {
+// sample.c:153-178 over the first positions of the (p desc, id asc) order: pf(i) is the
+// probability and idf(i) the id at position i (in-window candidates come first).
+// Positions [0, E) are known to be positions of the full order; nwin is the window size.
+// Returns false (nothing consumed) when the cuts or the draw would read a position >= E;
+// otherwise advances rs and fills id and d.  Every loop index is uniform, so a wavefront
+// can run it with pf/idf reading lanes.
+template <typename PF, typename IF>
+__device__ __forceinline__ bool decide_prefix_f(PF &&pf, IF &&idf, int E, int nwin,
+                                                const qs_row_param &P, uint64_t &rs, int &id,
+                                                qs_pick_diag &d) {
     if (E < 1) return false;
     int n = nwin;                                             // sample.c:153-154
     if (P.top_k > 0 && P.top_k < n) n = P.top_k;
@@ -307,40 +311,47 @@ __device__ __forceinline__ bool decide_prefix(const uint64_t *srt, int E, int nw
         int keep = n;
         for (int i = 0; i < n; ++i) {
             if (i >= E) return false;
-            cum += key_p(srt[i]);
+            cum += pf(i);
             if (cum >= P.top_p) { keep = i + 1; break; }
         }
         n = keep;
     }
     d.keep_topp = n;
     if (P.min_p > 0.0f) {                                     // sample.c:161-168
-        const float floor_p = P.min_p * key_p(srt[0]);
+        const float floor_p = P.min_p * pf(0);
         int keep = n;
         for (int i = 1; i < n; ++i) {
             if (i >= E) return false;
-            if (key_p(srt[i]) < floor_p) { keep = i; break; }
+            if (pf(i) < floor_p) { keep = i; break; }
         }
         n = keep;
     }
     if (n < 1) n = 1;
     if (n > E) return false;
     double rsum = 0.0;                                        // sample.c:170-175
-    for (int i = 0; i < n; ++i) rsum += key_p(srt[i]);
+    for (int i = 0; i < n; ++i) rsum += pf(i);
     const double u = rng_unit(rs);
     const double r = u * rsum;
     double acc = 0.0;
     int rank = n - 1;
     for (int i = 0; i < n; ++i) {
-        acc += key_p(srt[i]);
+        acc += pf(i);
         if (r <= acc) { rank = i; break; }
     }
-    id = key_id(srt[rank]);
+    id = idf(rank);
     d.keep = n;
     d.rank = rank;
     d.rsum = rsum;
     d.u = u;
-    d.p0 = key_p(srt[0]);
+    d.p0 = pf(0);
     return true;
+}
+
+__device__ __forceinline__ bool decide_prefix(const uint64_t *srt, int E, int nwin,
+                                              const qs_row_param &P, uint64_t &rs, int &id,
+                                              qs_pick_diag &d) {
+    return decide_prefix_f([&](int i) { return key_p(srt[i]); },
+                           [&](int i) { return key_id(srt[i]); }, E, nwin, P, rs, id, d);
 }
 
 // ---- the full-window path ------------------------------------------------------------------
@@ -716,6 +727,158 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
         __syncthreads();
     }
     if (full) full_row<NT>(x, V, row, P, t.maxl, t.sum, st, sc, out, diag, tab, fl, fixed_slot);
+}
+
+// ---- the decision by one wavefront ----------------------------------------------------------
+
+constexpr int WAVE_CAND = 256;   // candidates the one-wavefront decision takes (4 per lane)
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int i) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, i);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), i);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// decide_row's decision for one row by one wavefront, in registers: the K-th largest
+// candidate key by a bit-serial ballot select, exact p per lane, a 64-lane bitonic sort by
+// (p desc, id asc), the proof of the prefix and sample.c:153-178 through lane reads.  For
+// rows with at most WAVE_CAND gathered candidates whose top K (ties kept) are at most 64.
+// Returns 0 when the row is decided and recorded, 1 when it needs decide_row (too many
+// candidates, non-finite maximum, overflowed lists), 2 when the proof does not cover the
+// cuts (the caller runs full_row).  scratch: 64 u64 of LDS private to this wavefront.
+__device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, const RowTotals &t,
+                                               const uint32_t *keys, const int32_t *ids,
+                                               uint64_t *scratch, const uint64_t *tab,
+                                               const RowState &st, int32_t *out,
+                                               qs_pick_diag *diag) {
+    const int lane = threadIdx.x & 63;
+    const float inv_t = P.inv_t;
+    const float msc = t.maxl * inv_t;
+    const float thr = msc - 30.0f;
+    if (!isfinite(msc) || t.cflag || t.total > WAVE_CAND) return 1;
+    uint64_t rs = st.rng[row];                     // in flight during the selection
+    uint32_t k[4];
+    int idv[4];
+    bool valid[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int j = q * 64 + lane;
+        valid[q] = j < t.total;
+        k[q] = valid[q] ? keys[j] : 0u;
+        idv[q] = valid[q] ? ids[j] : 0;
+    }
+    // the K-th largest key (ties kept above it), as block_kth does
+    const int K = row_ksel(P);
+    uint32_t th = 0u;
+    if (t.total > K) {
+        for (int b = 31; b >= 0; --b) {
+            const uint32_t c = th | (1u << b);
+            int cnt = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) cnt += __popcll(__ballot(valid[q] && k[q] >= c));
+            if (cnt >= K) th = c;
+        }
+    }
+    int n_kept = 0;
+    uint32_t myrej = 0u;
+    bool keep[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        keep[q] = valid[q] && k[q] >= th;
+        if (valid[q] && !keep[q]) myrej = k[q] > myrej ? k[q] : myrej;
+        n_kept += __popcll(__ballot(keep[q]));
+    }
+    if (n_kept > 64) return 1;
+    const uint32_t wrej = wave_max_u(myrej);
+    const uint32_t rej = t.rej > wrej ? t.rej : wrej;
+    // the kept candidates, one per lane
+    int base = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint64_t m = __ballot(keep[q]);
+        if (keep[q]) scratch[base + lane_prefix(m)] = ((uint64_t)k[q] << 32) | (uint32_t)idv[q];
+        base += __popcll(m);
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float inv = (float)(1.0 / t.sum);
+    uint64_t pk = 0ull;                            // out of the window: sorts last
+    if (lane < n_kept) {
+        const uint64_t e = scratch[lane];
+        const float s = key2f((uint32_t)(e >> 32)) * inv_t;
+        if (s >= thr) pk = pid_key(qs_expf_core(s - msc, tab) * inv, (int)(uint32_t)e);
+    }
+    for (int size = 2; size <= 64; size <<= 1) {   // bitonic, descending
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint64_t o = shfl_xor_u64(pk, stride);
+            const bool take_max = ((lane & stride) == 0) == ((lane & size) == 0);
+            pk = take_max ? (o > pk ? o : pk) : (o < pk ? o : pk);
+        }
+    }
+    const int m = __popcll(__ballot((pk >> 32) != 0ull));
+    // the largest probability any rejected logit can have (p is monotone in it)
+    float p_rej = -1.0f;
+    if (rej > KEY_NEG_INF) {
+        const float s = key2f(rej) * inv_t;
+        if (s >= thr) p_rej = qs_expf_core(s - msc, tab) * inv;
+    }
+    int E = m;
+    if (m < t.nwin) {
+        const uint64_t below = __ballot(lane < m && key_p(pk) <= p_rej);
+        if (below) E = __builtin_ctzll(below);
+    }
+    qs_pick_diag d;
+    memset(&d, 0, sizeof d);
+    int id = -1;
+    const bool ok = decide_prefix_f([&](int i) { return key_p(lane_u64(pk, i)); },
+                                    [&](int i) { return key_id(lane_u64(pk, i)); }, E, t.nwin,
+                                    P, rs, id, d);
+    if (!ok) return 2;
+    if (lane == 0) {
+        int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+        st.rng[row] = rs;
+        ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
+        out[row] = id;
+        if (diag) {
+            d.id = id;
+            d.path = QS_PATH_FAST;
+            d.n_window = t.nwin;
+            d.n_cand = m;
+            d.maxl = t.maxl;
+            d.msc = msc;
+            d.inv = inv;
+            d.sum = t.sum;
+            diag[row] = d;
+        }
+    }
+    return 0;
+}
+
+// decide_row with the one-wavefront decision first: all threads of the block call it,
+// with the gathered candidates in keys/ids (LDS) and the block synchronised.
+template <int NT, int SC = SORT_CAP>
+__device__ __forceinline__ void decide_row_fast(int row, const qs_row_param &P, const RowTotals &t,
+                                                int fcap, uint32_t *keys, int32_t *ids,
+                                                uint64_t *srt, DecideLds<NT> &dl,
+                                                FullLds<NT> &fl, const float *x, int V,
+                                                const RowState &st, const Scratch &sc,
+                                                int32_t *out, qs_pick_diag *diag,
+                                                int fixed_slot) {
+    if (threadIdx.x < 64) {
+        const int status = decide_row_wave(row, P, t, keys, ids, srt, dl.tab, st, out, diag);
+        if (threadIdx.x == 0) dl.sh[7] = status;
+    }
+    __syncthreads();
+    const int status = dl.sh[7];
+    __syncthreads();
+    if (status == 1)
+        decide_row<NT, SC>(row, P, t, fcap, keys, ids, srt, dl, fl, x, V, st, sc, out, diag,
+                           fixed_slot);
+    else if (status == 2)
+        full_row<NT>(x, V, row, P, t.maxl, t.sum, st, sc, out, diag, dl.tab, fl, fixed_slot);
 }
 
 // sample.c:130-134 from per-slice (value, first index) bests: nothing beats a NaN at index

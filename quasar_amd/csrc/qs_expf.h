@@ -50,15 +50,26 @@ QS_EXPF_FN uint64_t qs_d2u(double d) { union { double d; uint64_t u; } c; c.d = 
 QS_EXPF_FN double qs_u2d(uint64_t u) { union { double d; uint64_t u; } c; c.u = u; return c.d; }
 
 /* Core for |x| < 88 (and the sub-range [-103.97, -88] that still rounds to a subnormal):
- * no special-case tests. */
+ * no special-case tests.  Adding ki << 47 to a table entry leaves its low word unchanged
+ * and adds (ki << 15) mod 2^32 to its high word; the device code does exactly that with
+ * one 32-bit shift-add (written as such, since the compiler would otherwise widen it back
+ * to a 64-bit add). */
 QS_EXPF_FN float qs_expf_core(float x, const uint64_t *tab) {
     double xd = (double)x;
     double kd = __builtin_fma(QS_EXPF_INVLN2N, xd, QS_EXPF_SHIFT);
     uint64_t ki = qs_d2u(kd);
     kd = kd - QS_EXPF_SHIFT;
     double r = __builtin_fma(QS_EXPF_INVLN2N, xd, -kd);
+#ifdef __HIP_DEVICE_COMPILE__
+    const uint64_t te = tab[ki & (QS_EXPF_TAB_N - 1)];
+    const uint32_t klo = (uint32_t)ki, tlo = (uint32_t)te;
+    uint32_t thi = (uint32_t)(te >> 32);
+    asm("v_lshl_add_u32 %0, %1, 15, %0" : "+v"(thi) : "v"(klo));
+    double s = qs_u2d(((uint64_t)thi << 32) | tlo);
+#else
     uint64_t t = tab[ki & (QS_EXPF_TAB_N - 1)] + (ki << 47);
     double s = qs_u2d(t);
+#endif
     double z = __builtin_fma(QS_EXPF_C0, r, QS_EXPF_C1);
     double r2 = r * r;
     double y = __builtin_fma(QS_EXPF_C2, r, 1.0);

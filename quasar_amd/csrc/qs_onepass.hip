@@ -228,8 +228,8 @@ __device__ __forceinline__ void finalize_row(const OpArgs &a, int row, const qs_
         }
     }
     __syncthreads();
-    decide_row<NT, SORTN>(row, P, t, FIN, f.keys, f.ids, f.srt, f.dl, f.fl, x, a.vocab,
-                          a.st, a.sc, a.out, a.diag, -1);
+    decide_row_fast<NT, SORTN>(row, P, t, FIN, f.keys, f.ids, f.srt, f.dl, f.fl, x, a.vocab,
+                               a.st, a.sc, a.out, a.diag, -1);
     if (tid == 0) reset_row(a, row);
 }
 

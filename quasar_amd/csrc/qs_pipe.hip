@@ -13,18 +13,19 @@
 // Per stage:
 //
 //   data waves                              control wave
-//   sum(s): w*inv_t, window, libm-equal     publish max(s+1); wait for the row's eight
-//   expf, double partial sums, candidates   maxima of s+1 (bounded); threshold(s+1);
-//   at or above threshold(s)                history bitmap for part s+2
+//   sum(s): w*inv_t, window, libm-equal     publish the max of part s+1 (completed last
+//   expf, double partial sums, candidates   stage); history bitmap for part s+2
+//   at or above threshold(s)
 //   -------------------------------------- barrier --------------------------------------
-//   complete(s+2): penalty, thread maxima,  store part s's sums and candidates, release
-//   part max; issue loads of part s+3       them
+//   complete(s+2): penalty, part max,       store part s's sums and candidates; read the
+//   threshold(s+2) (per-wave ballot select  row max of part s+1, published half a stage
+//   over lane maxima); loads of part s+3    earlier by all eight partners
 //   -------------------------------------- barrier --------------------------------------
 //
-// so the waits, the threshold select and the stores overlap the data waves' work, and a
-// wave's memory counter never covers another wave's loads.  After the last stage each
-// workgroup finishes rows r = w (mod G) with decide_row (k_finalize's logic), using its
-// own full-window scratch slot.
+// so the row-max exchange has half a stage to travel, the stores overlap the data waves'
+// work, and a wave's memory counter never covers another wave's loads.  After the last
+// stage each workgroup finishes rows r = w (mod G) with decide_row_fast, using its own
+// full-window scratch slot.
 //
 // Every wait is bounded (SPIN_LIMIT polls): one that gives up sets the sticky error flag
 // and the pick reports an error instead of hanging.  A workgroup only waits for
@@ -51,7 +52,7 @@ constexpr int NWV = NT / 64;         // wavefronts
 constexpr int DT = NT - 64;          // data threads (waves 1..15)
 constexpr int PARTS = 8;             // parts per row
 constexpr int UP = 5;                // float4 per data thread per part
-constexpr int PCAP = 2048;           // candidates per part (== Scratch::ccap)
+constexpr int PCAP = 512;            // candidates per part (<= Scratch::ccap)
 constexpr int FCAP = 4096;           // candidates gathered per row in the epilogue
 
 __constant__ uint64_t c_exp_tab_p[QS_EXPF_TAB_N] = QS_EXPF_TABLE_INIT;
@@ -72,15 +73,16 @@ struct PipeArgs {
 // Shared state of one workgroup besides the dynamic region.
 struct PipeLds {
     DecideLds<NT> dl;
-    float wmax[NWV];                 // per-wave part max of the part being completed
-    float wbv[NWV];                  // greedy: per-wave best value / index
-    int wbi[NWV];
-    double wsum[NWV];                // per-wave partial sums of the part being summed
-    int wcnt[NWV];                   // per-wave window counts
-    int wovf;                        // candidate buffer overflowed
-    int ncand;                       // candidates in the LDS buffer
-    uint32_t maxkey[2];              // row max key of parts s and s+1, by stage parity
-    uint32_t theta[2];               // candidate threshold keys, by stage parity
+    // hand-offs between the data waves and the control wave, double-buffered by part
+    // parity: written for one part while the other part's copy is read
+    float wmax[2][NWV];              // per-wave part max of a completed part
+    float wbv[2][NWV];               // greedy: per-wave best value / index
+    int wbi[2][NWV];
+    double wsum[2][NWV];             // per-wave partial sums of a summed part
+    int wcnt[2][NWV];                // per-wave window counts
+    int ncand[2];                    // candidates in the LDS lists
+    uint32_t maxkey[3];              // row max keys (by part index mod 3)
+    uint32_t theta[4];               // candidate threshold keys (by part index mod 4)
     RowTotals tot;
     int offs[PARTS + 1];
     float gbv;
@@ -93,6 +95,23 @@ struct Geo {                         // this workgroup's part of every row
 
 __device__ __forceinline__ int task_row(int s, int w, int rps) { return s * rps + (w % rps); }
 
+// The data thread index, opaque to the compiler: each stage recomputes its few per-float4
+// indices instead of the compiler keeping all of them (for all three buffer roles) live
+// across the stage loop, which does not fit beside the three part buffers.
+__device__ __forceinline__ int data_tid() {
+    int dt = (int)threadIdx.x - 64;
+    asm volatile("" : "+v"(dt));
+    return dt;
+}
+
+// Candidates a part keeps: about twice its share of the row's top K plus a margin (the
+// decision proves whatever it gets; a row whose top K crowd into one part takes the
+// full-window path).
+__device__ __forceinline__ int part_k(const qs_row_param &P) {
+    const int k = 2 * ((row_ksel(P) + PARTS - 1) / PARTS) + 8;
+    return k < DT ? k : DT;
+}
+
 __device__ __forceinline__ bool task_valid(const PipeArgs &a, int s, const Geo &g, int w) {
     return s < a.stages && task_row(s, w, g.rps) < a.n_rows;
 }
@@ -102,7 +121,7 @@ __device__ __forceinline__ bool task_valid(const PipeArgs &a, int s, const Geo &
 __device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a, int row,
                                             const Geo &g) {
     const float4 *x4 = (const float4 *)(a.logits + (int64_t)row * a.stride);
-    const int dt = (int)threadIdx.x - 64;
+    const int dt = data_tid();
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
         const int c = g.c_lo + u * DT + dt;
@@ -110,21 +129,25 @@ __device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a
     }
 }
 
-// Data waves: penalty, thread maxima (into tm), per-wave part max (greedy: best).
+// Data waves: penalty (sample.c:118-128), per-wave part max (greedy: first argmax) and the
+// part's candidate threshold: each data wave takes the kw-th largest of its 64 lane
+// maxima (kw distinct logits reach it) and the part keeps the smallest of those, so at
+// least 15*kw logits of the part reach it and every other one lies below it.
 __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const PipeArgs &a, int row,
-                                              const Geo &g, const uint32_t *bm, uint32_t *tm,
-                                              PipeLds &pl) {
+                                              const Geo &g, const uint32_t *bm,
+                                              uint32_t *theta, PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const qs_row_param P = a.st.prm[row];
     const float rp = P.repeat_penalty;
     const bool pen = rp > 1.0f && a.st.hlen[row] > 0 && P.ring_cap > 0;
     const bool greedy = row_greedy(P);
     const float qnan = __builtin_nanf("");
+    const int dt = data_tid();
     float mx = -INFINITY, bv = -INFINITY;
     int bi = -1;
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
-        const int c = g.c_lo + u * DT + (tid - 64);
+        const int c = g.c_lo + u * DT + dt;
         float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
         if (c >= g.c_hi) w[0] = w[1] = w[2] = w[3] = qnan;
         if (pen) {
@@ -148,90 +171,99 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const PipeArgs 
         }
         buf[u] = make_float4(w[0], w[1], w[2], w[3]);
     }
-    tm[tid - 64] = f2key(mx);
     const float m = wave_max_f(mx);
-    if (greedy) wave_best(bv, bi);
+    if (greedy) {
+        wave_best(bv, bi);
+    } else {
+        const int kw = (part_k(P) + (NWV - 2)) / (NWV - 1) + 1;
+        const uint32_t mk = f2key(mx);
+        uint32_t th = 0u;
+        for (int b = 31; b >= 0; --b) {
+            const uint32_t c = th | (1u << b);
+            if (__popcll(__ballot(mk >= c)) >= kw) th = c;
+        }
+        if (th <= KEY_NEG_INF) th = KEY_NEG_INF + 1u;       // -inf and NaN never qualify
+        if (lane == 0) atomicMin(theta, th);
+    }
     if (lane == 0) {
-        pl.wmax[wv] = m;
-        pl.wbv[wv] = bv;
-        pl.wbi[wv] = bi;
+        pl.wmax[par][wv] = m;
+        pl.wbv[par][wv] = bv;
+        pl.wbi[par][wv] = bi;
     }
 }
 
 // Data waves: exact softmax numerators, partial sums, window count and candidates of one
-// part, from registers (sample.c:136-149 per element).
+// part, from registers (sample.c:136-149 per element).  Out-of-window lanes evaluate the
+// exp core at X_OUT, which is exactly +0; a part whose float4 holds no logit at or above
+// the threshold skips the candidate test.
+constexpr float X_OUT = -150.0f;
+
 __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const PipeArgs &a, int row,
                                          const Geo &g, uint32_t *ckey, int32_t *cid,
-                                         uint32_t maxkey, uint32_t th, PipeLds &pl) {
+                                         uint32_t maxkey, uint32_t th, PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const qs_row_param P = a.st.prm[row];
     const float inv_t = P.inv_t;
     const float msc = key2f(maxkey) * inv_t;
     const float thr = msc - 30.0f;
     if (row_greedy(P) || !isfinite(msc)) return;   // decided in the epilogue
-    const float thf = th > KEY_NEG_INF ? key2f(th) : -INFINITY;
+    const float thf = key2f(th);
     const uint64_t *tab = pl.dl.tab;
-    double acc = 0.0;
+    float xo = X_OUT;
+    asm volatile("" : "+v"(xo));                    // a register, selected before the exp
+    double acc0 = 0.0, acc1 = 0.0;
     int cnt = 0;
-    int ovf = 0;
+    const int dt = data_tid();
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
-        const int c = g.c_lo + u * DT + (tid - 64);
-        const bool valid = c < g.c_hi;
+        const int c = g.c_lo + u * DT + dt;
         const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
-        float s[4];
-        bool in[4], cand[4];
+        float sc[4];
+        bool in[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            s[k] = w[k] * inv_t;
-            in[k] = valid && s[k] >= thr;
-            cand[k] = valid && w[k] >= thf;
+            sc[k] = w[k] * inv_t;
+            in[k] = sc[k] >= thr;                   // NaN (masked or past the part) is out
             cnt += __popcll(__ballot(in[k]));
         }
         if (__ballot(in[0] | in[1] | in[2] | in[3])) {
+            float e[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float e = qs_expf_core(s[k] - msc, tab);
-                acc += in[k] ? (double)e : 0.0;
-            }
+            for (int k = 0; k < 4; ++k) e[k] = qs_expf_core(in[k] ? sc[k] - msc : xo, tab);
+            acc0 += (double)e[0];
+            acc1 += (double)e[1];
+            acc0 += (double)e[2];
+            acc1 += (double)e[3];
         }
-        if (__ballot(cand[0] | cand[1] | cand[2] | cand[3])) {
+        const float m4 = fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3]));
+        if (__ballot(m4 >= thf)) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint64_t mk = __ballot(cand[k]);
-                if (mk) {
-                    int base = 0;
-                    if (lane == 0) base = atomicAdd(&pl.ncand, __popcll(mk));
-                    base = __shfl(base, 0, 64);
-                    if (cand[k]) {
-                        const int pos = base + lane_prefix(mk);
-                        if (pos < PCAP) {
-                            ckey[pos] = f2key(w[k]);
-                            cid[pos] = 4 * c + k;
-                        } else {
-                            ovf = 1;
-                        }
+                if (w[k] >= thf) {
+                    const int pos = atomicAdd(&pl.ncand[par], 1);
+                    if (pos < PCAP) {
+                        ckey[pos] = f2key(w[k]);
+                        cid[pos] = 4 * c + k;
                     }
                 }
             }
         }
     }
-    const double sa = wave_sum_d(acc);
-    const int o = wave_or_i(ovf);
+    const double sa = wave_sum_d(acc0 + acc1);
     if (lane == 0) {
-        pl.wsum[wv] = sa;
-        pl.wcnt[wv] = cnt;             // the wave's count (sum of ballot popcounts)
-        if (o) pl.wovf = 1;
+        pl.wsum[par][wv] = sa;
+        pl.wcnt[par][wv] = cnt;        // the wave's count (sum of ballot popcounts)
     }
 }
 
 // Control wave: wait (bounded) until all parts of `row` published their max; its key.
-__device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row) {
+// `first` is an arrival count read earlier (its latency overlapped other work).
+__device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row, int first = -1) {
     const int lane = threadIdx.x & 63;
     uint32_t key = 0u;
     if (lane == 0) {
         int it = 0;
-        while (ld_dev(&a.sc.arrive[row]) < PARTS) {
+        while ((first >= PARTS ? (first = PARTS) : (first = ld_dev(&a.sc.arrive[row]))) < PARTS) {
             if (++it >= SPIN_LIMIT) {
                 atomicOr(a.sc.err, 2);
                 break;
@@ -241,29 +273,6 @@ __device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row) {
         key = ld_dev(&a.sc.rowmax[row]);
     }
     return __shfl(key, 0, 64);
-}
-
-// Control wave: a candidate threshold for n keys in LDS: the k-th largest key with its
-// low 16 bits cleared (so at least k keys reach it).  Bit-serial over the top 16 bits,
-// counting with ballots, so the counts never leave the scalar unit.
-__device__ __forceinline__ uint32_t wave_kth16_lds(const uint32_t *keys, int n, int k) {
-    const int lane = threadIdx.x & 63;
-    constexpr int PER = DT / 64;       // keys per lane (n <= DT)
-    uint32_t v[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int i = j * 64 + lane;
-        v[j] = i < n ? keys[i] : 0u;
-    }
-    uint32_t prefix = 0u;
-    for (int b = 31; b >= 16; --b) {
-        const uint32_t cand = prefix | (1u << b);
-        int c = 0;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) c += __popcll(__ballot(v[j] >= cand));
-        if (c >= k) prefix = cand;
-    }
-    return prefix;
 }
 
 // Control wave: the history ids of `row` (up to RING_PF per lane stay in registers, so
@@ -321,23 +330,23 @@ __device__ __forceinline__ void control_bitmap(uint32_t *bm, const PipeArgs &a, 
 
 // Control wave: publish the completed part's max (sampling) or best (greedy).
 __device__ __forceinline__ void control_publish(const PipeArgs &a, int row, const Geo &g,
-                                                PipeLds &pl) {
+                                                PipeLds &pl, int par) {
     const int lane = threadIdx.x & 63;
     if (lane != 0) return;
     const qs_row_param P = a.st.prm[row];
     const int li = row * PARTS + g.part;
     if (row_greedy(P)) {
-        float v0 = pl.wbv[1];
-        int i0 = pl.wbi[1];
-        for (int k = 2; k < NWV; ++k) best_combine(v0, i0, pl.wbv[k], pl.wbi[k]);
+        float v0 = pl.wbv[par][1];
+        int i0 = pl.wbi[par][1];
+        for (int k = 2; k < NWV; ++k) best_combine(v0, i0, pl.wbv[par][k], pl.wbi[par][k]);
         st_dev(&a.sc.bestv[li], v0);
         st_dev(&a.sc.besti[li], i0);
         stores_done();
         add_dev(&a.sc.done[row], 1);
         return;
     }
-    float t = pl.wmax[1];
-    for (int k = 2; k < NWV; ++k) t = fmaxf(t, pl.wmax[k]);
+    float t = pl.wmax[par][1];
+    for (int k = 2; k < NWV; ++k) t = fmaxf(t, pl.wmax[par][k]);
     __hip_atomic_fetch_max(&a.sc.rowmax[row], f2key(t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     stores_done();
     add_dev(&a.sc.arrive[row], 1);
@@ -347,13 +356,15 @@ __device__ __forceinline__ void control_publish(const PipeArgs &a, int row, cons
 __device__ __forceinline__ void control_store(const PipeArgs &a, int row, const Geo &g,
                                               uint32_t maxkey, uint32_t th,
                                               const uint32_t *ckey, const int32_t *cid,
-                                              PipeLds &pl) {
+                                              PipeLds &pl, int par) {
     const int lane = threadIdx.x & 63;
     const qs_row_param P = a.st.prm[row];
     if (row_greedy(P)) return;                    // published with its best already
     const int li = row * PARTS + g.part;
     const bool live = isfinite(key2f(maxkey) * P.inv_t);
-    const int n = live ? min(pl.ncand, PCAP) : 0;
+    const int nc = pl.ncand[par];
+    const int n = live ? min(nc, PCAP) : 0;
+    const int ovf = live && nc > PCAP;
     uint32_t *gk = a.sc.ckey + (int64_t)li * PCAP;
     int32_t *gi = a.sc.cid + (int64_t)li * PCAP;
     for (int j = lane; j < n; j += 64) {
@@ -365,20 +376,19 @@ __device__ __forceinline__ void control_store(const PipeArgs &a, int row, const 
         int ct = 0;
         if (live)
             for (int k = 1; k < NWV; ++k) {
-                t += pl.wsum[k];
-                ct += pl.wcnt[k];
+                t += pl.wsum[par][k];
+                ct += pl.wcnt[par][k];
             }
         st_dev(&a.sc.psum[li], t);
         st_dev(&a.sc.pcnt[li], ct);
         st_dev(&a.sc.ccnt[li], n);
-        st_dev(&a.sc.cflag[li], live ? pl.wovf : 0);
+        st_dev(&a.sc.cflag[li], ovf);
         st_dev(&a.sc.crej[li], (live && th > KEY_NEG_INF) ? th - 1u : 0u);
     }
     stores_done();                                // the whole wave's stores, then the count
     if (lane == 0) {
         add_dev(&a.sc.done[row], 1);
-        pl.ncand = 0;
-        pl.wovf = 0;
+        pl.ncand[par] = 0;
     }
 }
 
@@ -446,17 +456,35 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
         RowTotals t = pl.tot;
         t.total = pl.offs[PARTS];
         if (t.total <= FCAP && isfinite(t.maxl * P.inv_t)) {
-            for (int j = tid; j < t.total; j += NT) {
-                int p = 0;
-                while (j >= pl.offs[p + 1]) ++p;
-                const int64_t src = (int64_t)(l0 + p) * PCAP + (j - pl.offs[p]);
-                keys[j] = ld_dev(&sc.ckey[src]);
-                ids[j] = ld_dev(&sc.cid[src]);
+            // every load issued before any is stored to LDS
+            uint32_t kk[FCAP / NT];
+            int32_t ii[FCAP / NT];
+#pragma unroll
+            for (int q = 0; q < FCAP / NT; ++q) {
+                const int j = q * NT + tid;
+                kk[q] = 0u;
+                ii[q] = 0;
+                if (j < t.total) {
+                    int p = 0;
+#pragma unroll
+                    for (int o = 1; o < PARTS; ++o) p += j >= pl.offs[o] ? 1 : 0;
+                    const int64_t src = (int64_t)(l0 + p) * PCAP + (j - pl.offs[p]);
+                    kk[q] = ld_dev(&sc.ckey[src]);
+                    ii[q] = ld_dev(&sc.cid[src]);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < FCAP / NT; ++q) {
+                const int j = q * NT + tid;
+                if (j < t.total) {
+                    keys[j] = kk[q];
+                    ids[j] = ii[q];
+                }
             }
         }
         __syncthreads();
-        decide_row<NT>(row, P, t, FCAP, keys, ids, srt, pl.dl, fl, x, a.vocab, st, sc, a.out,
-                       a.diag, slot);
+        decide_row_fast<NT>(row, P, t, FCAP, keys, ids, srt, pl.dl, fl, x, a.vocab, st, sc,
+                            a.out, a.diag, slot);
     }
     __syncthreads();
     if (tid == 0) {                               // ready for the next pick
@@ -468,43 +496,42 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
 
 // One stage: `cur` holds the completed part s, `nxt` the completed part s+1, `ld` is
 // loading part s+2 (and receives part s+3 once `cur` is free: the caller rotates roles).
+// One stage (one barrier).  Data waves: sum part s, complete part s+2, issue the loads of
+// part s+3.  Control wave, meanwhile: publish part s+1's max (completed last stage), store
+// part s-1's sums and candidates, build part s+3's history bitmap, read part s+1's row
+// max.  Every hand-off crosses the barrier at the top of a stage into a slot the other
+// side is not using in that stage (parity for bitmaps, wave results and candidate lists;
+// part index mod 3 for row maxima, mod 4 for thresholds).
 __device__ __forceinline__ void stage(float4 (&cur)[UP], float4 (&ld)[UP], int s,
                                       const PipeArgs &a, const Geo &g, int w, uint32_t *bm,
-                                      uint32_t *ckey, int32_t *cid, uint32_t *tm0,
-                                      uint32_t *tm1, PipeLds &pl) {
+                                      uint32_t *ckey, int32_t *cid, PipeLds &pl) {
     const int tid = threadIdx.x;
     const bool data = tid >= 64;
     const bool v0 = task_valid(a, s, g, w), v1 = task_valid(a, s + 1, g, w),
                v2 = task_valid(a, s + 2, g, w), v3 = task_valid(a, s + 3, g, w);
     const int r0 = task_row(s, w, g.rps), r1 = task_row(s + 1, w, g.rps),
               r2 = task_row(s + 2, w, g.rps), r3 = task_row(s + 3, w, g.rps);
+    const int p0 = s & 1, p1 = p0 ^ 1;
     __syncthreads();
     if (data) {
-        if (v0) sum_part(cur, a, r0, g, ckey, cid, pl.maxkey[s & 1], pl.theta[s & 1], pl);
-    } else {
-        RingIds ring2;                           // in flight while publishing and polling
-        if (v2) ring2 = ring_fetch(a, r2);
-        if (v1) {
-            control_publish(a, r1, g, pl);       // part s+1 was completed last stage
-            if (!row_greedy(a.st.prm[r1])) {
-                const uint32_t key = poll_rowmax(a, r1);
-                const qs_row_param P1 = a.st.prm[r1];
-                const uint32_t th = wave_kth16_lds((s + 1) & 1 ? tm1 : tm0, DT,
-                                                 min(2 * row_ksel(P1), DT));
-                if ((tid & 63) == 0) {
-                    pl.maxkey[(s + 1) & 1] = key;
-                    pl.theta[(s + 1) & 1] = th;
-                }
-            }
-        }
-        if (v2) bitmap_build(bm, ring2, a, r2, g);
-    }
-    __syncthreads();
-    if (data) {
-        if (v2) complete_part(ld, a, r2, g, bm, (s & 1) ? tm1 : tm0, pl);
+        if (v0)
+            sum_part(cur, a, r0, g, ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
+                     pl.theta[s & 3], pl, p0);
+        if (v2) complete_part(ld, a, r2, g, bm + p0 * g.bm_words, &pl.theta[(s + 2) & 3], pl, p0);
         if (v3) issue_loads(cur, a, r3, g);
-    } else if (v0) {
-        control_store(a, r0, g, pl.maxkey[s & 1], pl.theta[s & 1], ckey, cid, pl);
+    } else {
+        RingIds ring3;                           // in flight while publishing and storing
+        if (v3) ring3 = ring_fetch(a, r3);
+        if (v1) control_publish(a, r1, g, pl, p1);
+        if (s >= 1 && task_valid(a, s - 1, g, w))
+            control_store(a, task_row(s - 1, w, g.rps), g, pl.maxkey[(s + 2) % 3],
+                          pl.theta[(s + 3) & 3], ckey + p1 * PCAP, cid + p1 * PCAP, pl, p1);
+        if ((tid & 63) == 0) pl.theta[(s + 3) & 3] = 0xFFFFFFFFu;   // for part s+3
+        if (v3) bitmap_build(bm + p1 * g.bm_words, ring3, a, r3, g);
+        if (v1 && !row_greedy(a.st.prm[r1])) {
+            const uint32_t key = poll_rowmax(a, r1);
+            if ((tid & 63) == 0) pl.maxkey[(s + 1) % 3] = key;
+        }
     }
 }
 
@@ -521,52 +548,57 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     g.c_lo = g.lo >> 2;
     g.c_hi = p_hi >> 2;
     g.bm_words = a.part_len / 32 + 1;
-    uint32_t *bm = dyn;
-    uint32_t *ckey = dyn + g.bm_words;
-    int32_t *cid = (int32_t *)(ckey + PCAP);
-    uint32_t *tm0 = (uint32_t *)(cid + PCAP);
-    uint32_t *tm1 = tm0 + DT;
+    uint32_t *bm = dyn;                              // [2][bm_words]
+    uint32_t *ckey = dyn + 2 * g.bm_words;           // [2][PCAP]
+    int32_t *cid = (int32_t *)(ckey + 2 * PCAP);     // [2][PCAP]
     if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];
-    if (tid == 0) { pl.ncand = 0; pl.wovf = 0; }
+    if (tid == 0) {
+        pl.ncand[0] = pl.ncand[1] = 0;
+        for (int q = 0; q < 4; ++q) pl.theta[q] = 0xFFFFFFFFu;
+    }
 
     float4 B0[UP], B1[UP], B2[UP];
-    // prologue: parts 0 and 1 completed and part 0's max known; part 2 loading
+    // prologue: parts 0 and 1 completed, part 0's row max known, part 2 loading and its
+    // bitmap built
     const bool t0 = task_valid(a, 0, g, w), t1 = task_valid(a, 1, g, w),
                t2 = task_valid(a, 2, g, w);
     const int r0 = task_row(0, w, g.rps), r1 = task_row(1, w, g.rps), r2 = task_row(2, w, g.rps);
     if (data) {
         if (t0) issue_loads(B0, a, r0, g);
         if (t1) issue_loads(B1, a, r1, g);
-    } else if (t0) {
-        control_bitmap(bm, a, r0, g);
+    } else {
+        if (t0) control_bitmap(bm, a, r0, g);
+        if (t1) control_bitmap(bm + g.bm_words, a, r1, g);
     }
     __syncthreads();
-    if (data && t0) complete_part(B0, a, r0, g, bm, tm0, pl);
-    __syncthreads();
     if (data) {
+        if (t0) complete_part(B0, a, r0, g, bm, &pl.theta[0], pl, 0);
+        if (t1) complete_part(B1, a, r1, g, bm + g.bm_words, &pl.theta[1], pl, 1);
         if (t2) issue_loads(B2, a, r2, g);
-    } else if (t0) {
-        control_publish(a, r0, g, pl);
-        if (t1) control_bitmap(bm, a, r1, g);
     }
     __syncthreads();
-    if (data) {
-        if (t1) complete_part(B1, a, r1, g, bm, tm1, pl);
-    } else if (t0 && !row_greedy(a.st.prm[r0])) {
-        const uint32_t key = poll_rowmax(a, r0);
-        const uint32_t th = wave_kth16_lds(tm0, DT, min(2 * row_ksel(a.st.prm[r0]), DT));
-        if ((tid & 63) == 0) {
-            pl.maxkey[0] = key;
-            pl.theta[0] = th;
+    if (!data) {
+        if (t0) control_publish(a, r0, g, pl, 0);
+        if (t2) control_bitmap(bm, a, r2, g);
+        if (t0 && !row_greedy(a.st.prm[r0])) {
+            const uint32_t key = poll_rowmax(a, r0);
+            if ((tid & 63) == 0) pl.maxkey[0] = key;
         }
     }
     // stages: buffer roles rotate with period 3
     for (int s = 0; s < a.stages; s += 3) {
-        stage(B0, B2, s, a, g, w, bm, ckey, cid, tm0, tm1, pl);
+        stage(B0, B2, s, a, g, w, bm, ckey, cid, pl);
         if (s + 1 >= a.stages) break;
-        stage(B1, B0, s + 1, a, g, w, bm, ckey, cid, tm0, tm1, pl);
+        stage(B1, B0, s + 1, a, g, w, bm, ckey, cid, pl);
         if (s + 2 >= a.stages) break;
-        stage(B2, B1, s + 2, a, g, w, bm, ckey, cid, tm0, tm1, pl);
+        stage(B2, B1, s + 2, a, g, w, bm, ckey, cid, pl);
+    }
+    __syncthreads();
+    {                                                // the last summed part
+        const int s = a.stages - 1;
+        if (!data && s >= 0 && task_valid(a, s, g, w))
+            control_store(a, task_row(s, w, g.rps), g, pl.maxkey[s % 3], pl.theta[s & 3],
+                          ckey + (s & 1) * PCAP, cid + (s & 1) * PCAP, pl, s & 1);
     }
     __syncthreads();
     // epilogue: rows r = w (mod G), each with this workgroup's full-window slot
@@ -587,7 +619,7 @@ int qs_pipe_supported(int n_rows, int n_vocab, int64_t row_stride, const void *l
 
 size_t qs_pipe_lds_bytes(int n_vocab) {
     const int part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
-    const size_t pipe = sizeof(uint32_t) * ((size_t)part_len / 32 + 1 + 2 * PCAP + 2 * DT);
+    const size_t pipe = sizeof(uint32_t) * (2 * ((size_t)part_len / 32 + 1) + 4 * PCAP);
     const size_t epi = sizeof(uint32_t) * 2 * FCAP + sizeof(uint64_t) * SORT_CAP;
     const size_t fl = sizeof(FullLds<NT>);
     size_t m = pipe > epi ? pipe : epi;

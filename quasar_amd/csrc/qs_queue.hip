@@ -324,8 +324,8 @@ __device__ __forceinline__ void finalize_sampling(const QArgs &a, int row, const
     }
     __syncthreads();
     const float *x = a.logits + (int64_t)row * a.stride;
-    decide_row<NT, SORTN>(row, P, t, FIN, f.keys, f.ids, f.srt, f.dl, f.fl, x, a.vocab,
-                          a.st, a.sc, a.out, a.diag, -1);
+    decide_row_fast<NT, SORTN>(row, P, t, FIN, f.keys, f.ids, f.srt, f.dl, f.fl, x, a.vocab,
+                               a.st, a.sc, a.out, a.diag, -1);
     if (tid == 0) reset_row(a, row);
 }
 
