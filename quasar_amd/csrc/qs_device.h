@@ -42,29 +42,152 @@ __device__ __forceinline__ int lane_prefix(uint64_t m) {
                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Wavefront reductions in DPP moves only (no LDS instruction, so they do not queue behind
+// other wavefronts' LDS traffic): pairs and quads by quad permutes, 8 and 16 lanes by the
+// half-row and row mirrors, then row 1 (3) takes row 0's (2's) lane 15 and rows 2-3 take
+// lane 31; lane 63 ends with the whole wavefront and is broadcast.  The combination order
+// is fixed by lane positions, so double sums do not depend on timing.
+template <int CTRL, int ROWS, typename T>
+__device__ __forceinline__ T dpp_move(T x) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+    if constexpr (sizeof(T) == 4) {
+        const int b = __builtin_bit_cast(int, x);
+        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(b, b, CTRL, ROWS, 0xF, false));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, x);
+        const int lo = (int)(uint32_t)u, hi = (int)(uint32_t)(u >> 32);
+        const uint32_t rlo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWS, 0xF, false);
+        const uint32_t rhi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWS, 0xF, false);
+        return __builtin_bit_cast(T, ((uint64_t)rhi << 32) | rlo);
+    }
 }
-// Butterfly over the wave: every lane ends with the same value and the rounding of the
-// double adds depends only on lane positions, never on timing.
+template <typename T, typename F>
+__device__ __forceinline__ T wave_reduce(T v, F &&op) {
+    v = op(v, dpp_move<0xB1, 0xF>(v));      // quad_perm [1,0,3,2]
+    v = op(v, dpp_move<0x4E, 0xF>(v));      // quad_perm [2,3,0,1]
+    v = op(v, dpp_move<0x141, 0xF>(v));     // row_half_mirror
+    v = op(v, dpp_move<0x140, 0xF>(v));     // row_mirror
+    v = op(v, dpp_move<0x142, 0xA>(v));     // row_bcast:15 into rows 1 and 3
+    v = op(v, dpp_move<0x143, 0xC>(v));     // row_bcast:31 into rows 2 and 3
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+    return wave_reduce(v, [](int a, int b) { return a + b; });
+}
 __device__ __forceinline__ double wave_sum_d(double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    return wave_reduce(v, [](double a, double b) { return a + b; });
 }
 __device__ __forceinline__ float wave_max_f(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t t = __shfl_xor(v, o, 64);
-        v = t > v ? t : v;
-    }
-    return v;
+    return wave_reduce(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+    return wave_reduce(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
 }
 __device__ __forceinline__ int wave_or_i(int v) {
-    for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+    return wave_reduce(v, [](int a, int b) { return a | b; });
+}
+
+// The value of lane (lane ^ S): DPP for S = 1, 2 (quad permutes) and 8 (a rotation by 8
+// within each row of 16 lanes), ds_swizzle in bit mode (xor within 32 lanes) for 4 and 16,
+// ds_bpermute for 32.
+template <int S>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (S == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (S == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (S == 8) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+    else if constexpr (S == 4 || S == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (S << 10));
+    else return (uint32_t)__shfl_xor((int)v, S, 64);
+}
+template <int S>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+    const uint32_t lo = xor_lane<S>((uint32_t)v), hi = xor_lane<S>((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// One compare-exchange step of a bitonic sort over the 64 lanes (descending overall).
+template <int SIZE, int S>
+__device__ __forceinline__ void bitonic_step(uint64_t &v, int lane) {
+    const uint64_t o = xor_lane64<S>(v);
+    const bool keep_max = ((lane & S) == 0) == ((lane & SIZE) == 0);
+    v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
+}
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v) {
+    const int lane = threadIdx.x & 63;
+    bitonic_step<2, 1>(v, lane);
+    bitonic_step<4, 2>(v, lane);   bitonic_step<4, 1>(v, lane);
+    bitonic_step<8, 4>(v, lane);   bitonic_step<8, 2>(v, lane);   bitonic_step<8, 1>(v, lane);
+    bitonic_step<16, 8>(v, lane);  bitonic_step<16, 4>(v, lane);  bitonic_step<16, 2>(v, lane);
+    bitonic_step<16, 1>(v, lane);
+    bitonic_step<32, 16>(v, lane); bitonic_step<32, 8>(v, lane);  bitonic_step<32, 4>(v, lane);
+    bitonic_step<32, 2>(v, lane);  bitonic_step<32, 1>(v, lane);
+    bitonic_step<64, 32>(v, lane); bitonic_step<64, 16>(v, lane); bitonic_step<64, 8>(v, lane);
+    bitonic_step<64, 4>(v, lane);  bitonic_step<64, 2>(v, lane);  bitonic_step<64, 1>(v, lane);
+    return v;
+}
+
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int i) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, i);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), i);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// The K-th largest of the keys a wavefront holds Q per lane (0: no key; keys are >= 1),
+// ties kept above it, i.e. the largest th with at least K keys >= th; `total` keys are
+// present.  Bit by bit from the highest bit where the largest and smallest keys differ
+// (the bits above it are common to all), stopping once exactly K keys lie at or above the
+// prefix: the K-th is then the least of them.  With total <= K, the least key.
+template <int Q>
+__device__ __forceinline__ uint32_t wave_kth(const uint32_t (&k)[Q], int K, int total) {
+    uint32_t kmx = 0u, kmn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        kmx = k[q] > kmx ? k[q] : kmx;
+        kmn = (k[q] != 0u && k[q] < kmn) ? k[q] : kmn;
+    }
+    kmx = wave_max_u(kmx);
+    kmn = wave_min_u(kmn);
+    if (kmx == kmn || total <= K) return kmn;
+    int b = 31 - __builtin_clz(kmx ^ kmn);
+    uint32_t th = kmx & ~((2u << b) - 1u);        // (2u << 31) wraps to 0: no common bits
+    int cur = total;                              // keys at or above th
+    for (; b >= 0 && cur != K; --b) {
+        const uint32_t c = th | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) cnt += __popcll(__ballot(k[q] >= c));
+        if (cnt >= K) {
+            th = c;
+            cur = cnt;
+        }
+    }
+    if (cur == K) {
+        uint32_t mn = 0xFFFFFFFFu;
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+            if (k[q] >= th) mn = k[q] < mn ? k[q] : mn;
+        th = wave_min_u(mn);
+    }
+    return th;
+}
+
+// Inclusive prefix sum over the lanes.
+__device__ __forceinline__ double wave_scan_d(double v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
     return v;
 }
 
@@ -352,6 +475,57 @@ __device__ __forceinline__ bool decide_prefix(const uint64_t *srt, int E, int nw
                                               qs_pick_diag &d) {
     return decide_prefix_f([&](int i) { return key_p(srt[i]); },
                            [&](int i) { return key_id(srt[i]); }, E, nwin, P, rs, id, d);
+}
+
+// decide_prefix_f for a wavefront whose lane i holds the (p, id) key of position i (lanes
+// past the candidates hold 0).  When every probability at positions below min(E, 64) is 0
+// or at least 2^-24, each is a multiple of 2^-47 and every partial sum of them lies below
+// 2, so binary64 holds every partial sum exactly: the running sums of sample.c:157, 171
+// and 174 then equal an inclusive lane scan (whatever the order of its additions) and
+// each cut is the first lane that passes its test.  Otherwise the sequential loops run.
+__device__ __forceinline__ bool decide_prefix_wave(uint64_t pk, int E, int nwin,
+                                                   const qs_row_param &P, uint64_t &rs,
+                                                   int &id, qs_pick_diag &d) {
+    const int lane = threadIdx.x & 63;
+    const float p = key_p(pk);
+    const int lim = E < 64 ? E : 64;
+    const bool inb = lane < lim;
+    if (__ballot(inb && p != 0.0f && !(p >= 0x1p-24f)))
+        return decide_prefix_f([&](int i) { return key_p(lane_u64(pk, i)); },
+                               [&](int i) { return key_id(lane_u64(pk, i)); }, E, nwin, P, rs,
+                               id, d);
+    if (E < 1) return false;
+    const double cum = wave_scan_d(inb ? (double)p : 0.0);
+    int n = nwin;                                             // sample.c:153-154
+    if (P.top_k > 0 && P.top_k < n) n = P.top_k;
+    d.keep_topk = n;
+    if (P.top_p < 1.0f) {                                     // sample.c:155-160
+        const uint64_t hit = __ballot(inb && lane < n && cum >= (double)P.top_p);
+        if (hit) n = __builtin_ctzll(hit) + 1;
+        else if (n > E) return false;
+    }
+    d.keep_topp = n;
+    const float p0 = __shfl(p, 0, 64);
+    if (P.min_p > 0.0f) {                                     // sample.c:161-168
+        const float floor_p = P.min_p * p0;
+        const uint64_t hit = __ballot(inb && lane >= 1 && lane < n && p < floor_p);
+        if (hit) n = __builtin_ctzll(hit);
+        else if (n > E) return false;
+    }
+    if (n < 1) n = 1;
+    if (n > E) return false;
+    const double rsum = __shfl(cum, n - 1, 64);               // sample.c:170-175
+    const double u = rng_unit(rs);
+    const double r = u * rsum;
+    const uint64_t hit = __ballot(lane < n && r <= cum);
+    const int rank = hit ? __builtin_ctzll(hit) : n - 1;
+    id = key_id(lane_u64(pk, rank));
+    d.keep = n;
+    d.rank = rank;
+    d.rsum = rsum;
+    d.u = u;
+    d.p0 = p0;
+    return true;
 }
 
 // ---- the full-window path ------------------------------------------------------------------
@@ -737,11 +911,6 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
     return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int i) {
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, i);
-    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), i);
-    return ((uint64_t)hi << 32) | lo;
-}
 
 // decide_row's decision for one row by one wavefront, in registers: the K-th largest
 // candidate key by a bit-serial ballot select, exact p per lane, a 64-lane bitonic sort by
@@ -775,13 +944,10 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
     const int K = row_ksel(P);
     uint32_t th = 0u;
     if (t.total > K) {
-        for (int b = 31; b >= 0; --b) {
-            const uint32_t c = th | (1u << b);
-            int cnt = 0;
+        uint32_t kk[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) cnt += __popcll(__ballot(valid[q] && k[q] >= c));
-            if (cnt >= K) th = c;
-        }
+        for (int q = 0; q < 4; ++q) kk[q] = valid[q] ? k[q] : 0u;
+        th = wave_kth(kk, K, t.total);
     }
     int n_kept = 0;
     uint32_t myrej = 0u;
@@ -811,13 +977,7 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
         const float s = key2f((uint32_t)(e >> 32)) * inv_t;
         if (s >= thr) pk = pid_key(qs_expf_core(s - msc, tab) * inv, (int)(uint32_t)e);
     }
-    for (int size = 2; size <= 64; size <<= 1) {   // bitonic, descending
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint64_t o = shfl_xor_u64(pk, stride);
-            const bool take_max = ((lane & stride) == 0) == ((lane & size) == 0);
-            pk = take_max ? (o > pk ? o : pk) : (o < pk ? o : pk);
-        }
-    }
+    pk = wave_sort_desc(pk);
     const int m = __popcll(__ballot((pk >> 32) != 0ull));
     // the largest probability any rejected logit can have (p is monotone in it)
     float p_rej = -1.0f;
@@ -833,9 +993,7 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
     qs_pick_diag d;
     memset(&d, 0, sizeof d);
     int id = -1;
-    const bool ok = decide_prefix_f([&](int i) { return key_p(lane_u64(pk, i)); },
-                                    [&](int i) { return key_id(lane_u64(pk, i)); }, E, t.nwin,
-                                    P, rs, id, d);
+    const bool ok = decide_prefix_wave(pk, E, t.nwin, P, rs, id, d);
     if (!ok) return 2;
     if (lane == 0) {
         int32_t *ring = st.ring + (int64_t)row * st.ring_stride;

@@ -54,6 +54,9 @@ constexpr int PARTS = 8;             // parts per row
 constexpr int UP = 5;                // float4 per data thread per part
 constexpr int PCAP = 512;            // candidates per part (<= Scratch::ccap)
 constexpr int FCAP = 4096;           // candidates gathered per row in the epilogue
+constexpr int TOPW_MAX = 16;         // thread maxima a data wave reports per part, at most
+constexpr int NDW = NWV - 1;         // data waves
+static_assert(TOPW_MAX * NDW <= 256, "the control wave holds the reports 4 per lane");
 
 __constant__ uint64_t c_exp_tab_p[QS_EXPF_TAB_N] = QS_EXPF_TABLE_INIT;
 
@@ -70,6 +73,18 @@ struct PipeArgs {
     qs_pick_diag *diag;
 };
 
+// What the data waves need of a part's row, copied to LDS by the control wave: the data
+// waves then issue no global reads besides the logits (a read of anything else would make
+// their waits also cover the logit loads issued before it).
+struct PartCfg {
+    float inv_t;
+    float rp;                        // repeat penalty
+    int flags;                       // CFG_GREEDY | CFG_PEN
+    int kw;                          // candidates the part keeps at least (part_k)
+    int tw;                          // thread maxima each data wave reports
+};
+constexpr int CFG_GREEDY = 1, CFG_PEN = 2;
+
 // Shared state of one workgroup besides the dynamic region.
 struct PipeLds {
     DecideLds<NT> dl;
@@ -83,6 +98,9 @@ struct PipeLds {
     int ncand[2];                    // candidates in the LDS lists
     uint32_t maxkey[3];              // row max keys (by part index mod 3)
     uint32_t theta[4];               // candidate threshold keys (by part index mod 4)
+    PartCfg cfg[4];                  // by part index mod 4
+    uint32_t wtop[2][TOPW_MAX * NDW];    // data waves' largest thread maxima (by parity;
+                                         // report i of wave w at i * NDW + w - 1)
     RowTotals tot;
     int offs[PARTS + 1];
     float gbv;
@@ -116,31 +134,43 @@ __device__ __forceinline__ bool task_valid(const PipeArgs &a, int s, const Geo &
     return s < a.stages && task_row(s, w, g.rps) < a.n_rows;
 }
 
+// Control wave: the settings of `row` for the data waves.
+__device__ __forceinline__ void set_cfg(PartCfg &c, const PipeArgs &a, int row) {
+    if ((threadIdx.x & 63) != 0) return;
+    const qs_row_param P = a.st.prm[row];
+    const bool pen = P.repeat_penalty > 1.0f && a.st.hlen[row] > 0 && P.ring_cap > 0;
+    c.inv_t = P.inv_t;
+    c.rp = P.repeat_penalty;
+    c.flags = (row_greedy(P) ? CFG_GREEDY : 0) | (pen ? CFG_PEN : 0);
+    c.kw = part_k(P);
+    c.tw = min((c.kw + NDW - 1) / NDW + 1, TOPW_MAX);
+}
+
 // Data waves: loads of one part into registers (float4 c = c_lo + u*DT + dt; lanes past
-// the part read the part's last float4, and are masked later).
+// the part read the part's last float4, and are masked later).  Every stage issues the
+// same UP loads, so each wave's memory counter names exactly the loads a use waits for;
+// a stage with no part (past the last row) reads row 0's first float4 in every lane.
 __device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a, int row,
-                                            const Geo &g) {
-    const float4 *x4 = (const float4 *)(a.logits + (int64_t)row * a.stride);
+                                            bool live, const Geo &g) {
+    const float4 *x4 = (const float4 *)(a.logits + (live ? (int64_t)row * a.stride : 0));
     const int dt = data_tid();
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
         const int c = g.c_lo + u * DT + dt;
-        buf[u] = x4[c < g.c_hi ? c : g.c_hi - 1];
+        buf[u] = x4[live ? (c < g.c_hi ? c : g.c_hi - 1) : 0];
     }
 }
 
 // Data waves: penalty (sample.c:118-128), per-wave part max (greedy: first argmax) and the
-// part's candidate threshold: each data wave takes the kw-th largest of its 64 lane
-// maxima (kw distinct logits reach it) and the part keeps the smallest of those, so at
-// least 15*kw logits of the part reach it and every other one lies below it.
-__device__ __forceinline__ void complete_part(float4 (&buf)[UP], const PipeArgs &a, int row,
-                                              const Geo &g, const uint32_t *bm,
-                                              uint32_t *theta, PipeLds &pl, int par) {
+// wave's cf.tw largest thread maxima (keys of cf.tw distinct logits), from which the
+// control wave takes the part's candidate threshold.
+__device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
+                                              const uint32_t *bm, const PartCfg &cf,
+                                              PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const qs_row_param P = a.st.prm[row];
-    const float rp = P.repeat_penalty;
-    const bool pen = rp > 1.0f && a.st.hlen[row] > 0 && P.ring_cap > 0;
-    const bool greedy = row_greedy(P);
+    const float rp = cf.rp;
+    const bool pen = (cf.flags & CFG_PEN) != 0;
+    const bool greedy = (cf.flags & CFG_GREEDY) != 0;
     const float qnan = __builtin_nanf("");
     const int dt = data_tid();
     float mx = -INFINITY, bv = -INFINITY;
@@ -175,15 +205,13 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const PipeArgs 
     if (greedy) {
         wave_best(bv, bi);
     } else {
-        const int kw = (part_k(P) + (NWV - 2)) / (NWV - 1) + 1;
-        const uint32_t mk = f2key(mx);
-        uint32_t th = 0u;
-        for (int b = 31; b >= 0; --b) {
-            const uint32_t c = th | (1u << b);
-            if (__popcll(__ballot(mk >= c)) >= kw) th = c;
+        uint32_t key = f2key(mx);
+        for (int i = 0; i < cf.tw; ++i) {
+            const uint32_t top = wave_max_u(key);
+            if (lane == 0) pl.wtop[par][i * NDW + wv - 1] = top;
+            const int at = __builtin_ctzll(__ballot(key == top));
+            if (lane == at) key = 0u;                  // each lane reports at most once
         }
-        if (th <= KEY_NEG_INF) th = KEY_NEG_INF + 1u;       // -inf and NaN never qualify
-        if (lane == 0) atomicMin(theta, th);
     }
     if (lane == 0) {
         pl.wmax[par][wv] = m;
@@ -198,15 +226,14 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const PipeArgs 
 // the threshold skips the candidate test.
 constexpr float X_OUT = -150.0f;
 
-__device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const PipeArgs &a, int row,
-                                         const Geo &g, uint32_t *ckey, int32_t *cid,
+__device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
+                                         const PartCfg &cf, uint32_t *ckey, int32_t *cid,
                                          uint32_t maxkey, uint32_t th, PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const qs_row_param P = a.st.prm[row];
-    const float inv_t = P.inv_t;
+    const float inv_t = cf.inv_t;
     const float msc = key2f(maxkey) * inv_t;
     const float thr = msc - 30.0f;
-    if (row_greedy(P) || !isfinite(msc)) return;   // decided in the epilogue
+    if ((cf.flags & CFG_GREEDY) || !isfinite(msc)) return;   // decided in the epilogue
     const float thf = key2f(th);
     const uint64_t *tab = pl.dl.tab;
     float xo = X_OUT;
@@ -326,6 +353,19 @@ __device__ __forceinline__ void control_bitmap(uint32_t *bm, const PipeArgs &a, 
                                                const Geo &g) {
     const RingIds r = ring_fetch(a, row);
     bitmap_build(bm, r, a, row, g);
+}
+
+// Control wave: the part's candidate threshold, the kw-th largest of the thread maxima the
+// data waves reported (kw distinct logits of the part reach it; the part keeps every logit
+// at or above it, and every other one lies below it).
+__device__ __forceinline__ uint32_t part_theta(const uint32_t *wtop, const PartCfg &cf) {
+    const int n = cf.tw * NDW;
+    const int lane = threadIdx.x & 63;
+    uint32_t k[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) k[q] = q * 64 + lane < n ? wtop[q * 64 + lane] : 0u;
+    const uint32_t th = wave_kth(k, cf.kw, n);
+    return th <= KEY_NEG_INF ? KEY_NEG_INF + 1u : th;   // -inf and NaN never qualify
 }
 
 // Control wave: publish the completed part's max (sampling) or best (greedy).
@@ -494,44 +534,54 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
     }
 }
 
-// One stage: `cur` holds the completed part s, `nxt` the completed part s+1, `ld` is
-// loading part s+2 (and receives part s+3 once `cur` is free: the caller rotates roles).
-// One stage (one barrier).  Data waves: sum part s, complete part s+2, issue the loads of
-// part s+3.  Control wave, meanwhile: publish part s+1's max (completed last stage), store
-// part s-1's sums and candidates, build part s+3's history bitmap, read part s+1's row
-// max.  Every hand-off crosses the barrier at the top of a stage into a slot the other
-// side is not using in that stage (parity for bitmaps, wave results and candidate lists;
-// part index mod 3 for row maxima, mod 4 for thresholds).
-__device__ __forceinline__ void stage(float4 (&cur)[UP], float4 (&ld)[UP], int s,
-                                      const PipeArgs &a, const Geo &g, int w, uint32_t *bm,
-                                      uint32_t *ckey, int32_t *cid, PipeLds &pl) {
-    const int tid = threadIdx.x;
-    const bool data = tid >= 64;
-    const bool v0 = task_valid(a, s, g, w), v1 = task_valid(a, s + 1, g, w),
-               v2 = task_valid(a, s + 2, g, w), v3 = task_valid(a, s + 3, g, w);
-    const int r0 = task_row(s, w, g.rps), r1 = task_row(s + 1, w, g.rps),
-              r2 = task_row(s + 2, w, g.rps), r3 = task_row(s + 3, w, g.rps);
-    const int p0 = s & 1, p1 = p0 ^ 1;
+// One stage, data waves: sum part s (in `cur`), issue the loads of part s+3 into `cur`,
+// complete part s+2 (in `ld`, loaded during the previous stage).
+__device__ __forceinline__ void data_stage(float4 (&cur)[UP], float4 (&ld)[UP], int s,
+                                           const PipeArgs &a, const Geo &g, int w,
+                                           const uint32_t *bm, uint32_t *ckey, int32_t *cid,
+                                           PipeLds &pl) {
+    const bool v0 = task_valid(a, s, g, w), v2 = task_valid(a, s + 2, g, w),
+               v3 = task_valid(a, s + 3, g, w);
+    const int r3 = task_row(s + 3, w, g.rps);
+    const int p0 = s & 1;
     __syncthreads();
-    if (data) {
-        if (v0)
-            sum_part(cur, a, r0, g, ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
-                     pl.theta[s & 3], pl, p0);
-        if (v2) complete_part(ld, a, r2, g, bm + p0 * g.bm_words, &pl.theta[(s + 2) & 3], pl, p0);
-        if (v3) issue_loads(cur, a, r3, g);
-    } else {
-        RingIds ring3;                           // in flight while publishing and storing
-        if (v3) ring3 = ring_fetch(a, r3);
-        if (v1) control_publish(a, r1, g, pl, p1);
-        if (s >= 1 && task_valid(a, s - 1, g, w))
-            control_store(a, task_row(s - 1, w, g.rps), g, pl.maxkey[(s + 2) % 3],
-                          pl.theta[(s + 3) & 3], ckey + p1 * PCAP, cid + p1 * PCAP, pl, p1);
-        if ((tid & 63) == 0) pl.theta[(s + 3) & 3] = 0xFFFFFFFFu;   // for part s+3
-        if (v3) bitmap_build(bm + p1 * g.bm_words, ring3, a, r3, g);
-        if (v1 && !row_greedy(a.st.prm[r1])) {
-            const uint32_t key = poll_rowmax(a, r1);
-            if ((tid & 63) == 0) pl.maxkey[(s + 1) % 3] = key;
-        }
+    if (v0)
+        sum_part(cur, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
+                 pl.theta[s & 3], pl, p0);
+    issue_loads(cur, a, r3, v3, g);
+    if (v2) complete_part(ld, g, bm + p0 * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
+}
+
+// One stage, control wave: publish part s+1's max (completed during the previous stage),
+// store part s-1's sums and candidates, build part s+3's history bitmap, read part s+1's
+// row max.  Every hand-off crosses the barrier at the top of a stage into a slot the other
+// side does not use in that stage (parity for bitmaps, wave results and candidate lists;
+// part index mod 3 for row maxima, mod 4 for thresholds).
+__device__ __forceinline__ void control_stage(int s, const PipeArgs &a, const Geo &g, int w,
+                                              uint32_t *bm, const uint32_t *ckey,
+                                              const int32_t *cid, PipeLds &pl) {
+    const int lane = threadIdx.x & 63;
+    const bool v1 = task_valid(a, s + 1, g, w), v3 = task_valid(a, s + 3, g, w);
+    const int r1 = task_row(s + 1, w, g.rps), r3 = task_row(s + 3, w, g.rps);
+    const int p1 = (s & 1) ^ 1;
+    __syncthreads();
+    RingIds ring3;                               // in flight while publishing and storing
+    if (v3) {
+        ring3 = ring_fetch(a, r3);
+        set_cfg(pl.cfg[(s + 3) & 3], a, r3);
+    }
+    if (v1) control_publish(a, r1, g, pl, p1);
+    if (s >= 1 && task_valid(a, s - 1, g, w))
+        control_store(a, task_row(s - 1, w, g.rps), g, pl.maxkey[(s + 2) % 3],
+                      pl.theta[(s + 3) & 3], ckey + p1 * PCAP, cid + p1 * PCAP, pl, p1);
+    if (v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY)) {
+        const uint32_t th = part_theta(pl.wtop[p1], pl.cfg[(s + 1) & 3]);
+        if (lane == 0) pl.theta[(s + 1) & 3] = th;
+    }
+    if (v3) bitmap_build(bm + p1 * g.bm_words, ring3, a, r3, g);
+    if (v1 && !row_greedy(a.st.prm[r1])) {
+        const uint32_t key = poll_rowmax(a, r1);
+        if (lane == 0) pl.maxkey[(s + 1) % 3] = key;
     }
 }
 
@@ -552,47 +602,62 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     uint32_t *ckey = dyn + 2 * g.bm_words;           // [2][PCAP]
     int32_t *cid = (int32_t *)(ckey + 2 * PCAP);     // [2][PCAP]
     if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];
-    if (tid == 0) {
-        pl.ncand[0] = pl.ncand[1] = 0;
-        for (int q = 0; q < 4; ++q) pl.theta[q] = 0xFFFFFFFFu;
-    }
+    if (tid == 0) pl.ncand[0] = pl.ncand[1] = 0;
 
-    float4 B0[UP], B1[UP], B2[UP];
     // prologue: parts 0 and 1 completed, part 0's row max known, part 2 loading and its
-    // bitmap built
+    // bitmap built.  Data and control waves then run loops of their own (the branch is on
+    // the wavefront index, uniform in each wavefront), meeting at one barrier per stage.
     const bool t0 = task_valid(a, 0, g, w), t1 = task_valid(a, 1, g, w),
                t2 = task_valid(a, 2, g, w);
     const int r0 = task_row(0, w, g.rps), r1 = task_row(1, w, g.rps), r2 = task_row(2, w, g.rps);
-    if (data) {
-        if (t0) issue_loads(B0, a, r0, g);
-        if (t1) issue_loads(B1, a, r1, g);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave != 0) {
+        float4 B0[UP], B1[UP], B2[UP];
+        issue_loads(B0, a, r0, t0, g);
+        issue_loads(B1, a, r1, t1, g);
+        __syncthreads();
+        issue_loads(B2, a, r2, t2, g);
+        if (t0) complete_part(B0, g, bm, pl.cfg[0], pl, 0);
+        if (t1) complete_part(B1, g, bm + g.bm_words, pl.cfg[1], pl, 1);
+        __syncthreads();
+        // buffer roles rotate with period 3
+        for (int s = 0; s < a.stages; s += 3) {
+            data_stage(B0, B2, s, a, g, w, bm, ckey, cid, pl);
+            if (s + 1 >= a.stages) break;
+            data_stage(B1, B0, s + 1, a, g, w, bm, ckey, cid, pl);
+            if (s + 2 >= a.stages) break;
+            data_stage(B2, B1, s + 2, a, g, w, bm, ckey, cid, pl);
+        }
     } else {
-        if (t0) control_bitmap(bm, a, r0, g);
-        if (t1) control_bitmap(bm + g.bm_words, a, r1, g);
-    }
-    __syncthreads();
-    if (data) {
-        if (t0) complete_part(B0, a, r0, g, bm, &pl.theta[0], pl, 0);
-        if (t1) complete_part(B1, a, r1, g, bm + g.bm_words, &pl.theta[1], pl, 1);
-        if (t2) issue_loads(B2, a, r2, g);
-    }
-    __syncthreads();
-    if (!data) {
+        // the control wave's steps are on every stage's critical path: it issues ahead of
+        // the data wavefronts that share its SIMD
+        __builtin_amdgcn_s_setprio(3);
+        if (t0) {
+            set_cfg(pl.cfg[0], a, r0);
+            control_bitmap(bm, a, r0, g);
+        }
+        if (t1) {
+            set_cfg(pl.cfg[1], a, r1);
+            control_bitmap(bm + g.bm_words, a, r1, g);
+        }
+        __syncthreads();
+        __syncthreads();
         if (t0) control_publish(a, r0, g, pl, 0);
-        if (t2) control_bitmap(bm, a, r2, g);
+        if (t0 && !(pl.cfg[0].flags & CFG_GREEDY)) {
+            const uint32_t th = part_theta(pl.wtop[0], pl.cfg[0]);
+            if ((tid & 63) == 0) pl.theta[0] = th;
+        }
+        if (t2) {
+            set_cfg(pl.cfg[2], a, r2);
+            control_bitmap(bm, a, r2, g);
+        }
         if (t0 && !row_greedy(a.st.prm[r0])) {
             const uint32_t key = poll_rowmax(a, r0);
             if ((tid & 63) == 0) pl.maxkey[0] = key;
         }
+        for (int s = 0; s < a.stages; ++s) control_stage(s, a, g, w, bm, ckey, cid, pl);
     }
-    // stages: buffer roles rotate with period 3
-    for (int s = 0; s < a.stages; s += 3) {
-        stage(B0, B2, s, a, g, w, bm, ckey, cid, pl);
-        if (s + 1 >= a.stages) break;
-        stage(B1, B0, s + 1, a, g, w, bm, ckey, cid, pl);
-        if (s + 2 >= a.stages) break;
-        stage(B2, B1, s + 2, a, g, w, bm, ckey, cid, pl);
-    }
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     {                                                // the last summed part
         const int s = a.stages - 1;
