@@ -555,7 +555,7 @@ static void batch_release(qs_batch *b) {
     void *ptrs[] = {b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead, b->sc.smax,
                     b->sc.bestv, b->sc.besti, b->sc.sth, b->sc.ckey, b->sc.cid, b->sc.ccnt,
                     b->sc.crej, b->sc.cflag, b->sc.psum, b->sc.pcnt, b->sc.locks,
-                    b->sc.full_keys, b->sc.full_bm, b->sc.err, b->sc.rowmax, b->sc.arrive,
+                    b->sc.full_keys, b->sc.full_bm, b->sc.err, b->sc.rowmax,
                     b->sc.done, b->op.ctl, b->op.ctr, b->op.psum, b->op.pcnt, b->op.rej, b->op.ccnt,
                     b->op.ckey, b->op.cid, b->op.bestv, b->op.besti};
     for (void *p : ptrs)
@@ -574,14 +574,7 @@ static int batch_alloc(qs_batch *b) {
     if (many > sr) sr = many;
     if (qs_pipe_parts() * R > sr) sr = qs_pipe_parts() * R;   // pipelined kernel: per part
     b->slice_rows = sr;
-    int dev = 0, ncu = 0, coop = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess) {
-        qs_set_error("device attributes unavailable");
-        return QS_EDEVICE;
-    }
-    b->pipe_grid = coop ? ncu / qs_pipe_parts() * qs_pipe_parts() : 0;
+    b->pipe_grid = qs_pipe_grid(V);
     b->op_grid = qs_onepass_grid();
     b->q_grid = qs_queue_grid();
     if (const char *e = getenv("QS_QUEUE_LAG_ROWS")) b->q_lag = atoi(e);
@@ -613,8 +606,7 @@ static int batch_alloc(qs_batch *b) {
     if (!rc) rc = dev_alloc(&b->sc.full_keys, (size_t)b->sc.nslots * 2 * V, "full_keys");
     if (!rc) rc = dev_alloc(&b->sc.full_bm, (size_t)b->sc.nslots * (V / 32 + 1), "full_bm");
     if (!rc) rc = dev_alloc(&b->sc.err, 1, "err");
-    if (!rc) rc = dev_alloc(&b->sc.rowmax, R, "rowmax");
-    if (!rc) rc = dev_alloc(&b->sc.arrive, R, "arrive");
+    if (!rc) rc = dev_alloc(&b->sc.rowmax, (size_t)R * qs_pipe_parts(), "rowmax");
     if (!rc) rc = dev_alloc(&b->sc.done, R, "done");
     if (!rc) rc = dev_alloc(&b->op.ctl, 2, "queue tickets");
     if (!rc) rc = dev_alloc(&b->op.ctr, (size_t)R * QS_OP_CTR_STRIDE, "op counters");
@@ -629,8 +621,8 @@ static int batch_alloc(qs_batch *b) {
     if (!rc && hipMemset(b->op.ctr, 0, sizeof(uint32_t) * R * QS_OP_CTR_STRIDE) != hipSuccess)
         rc = QS_EDEVICE;
     if (!rc && hipMemset(b->op.ctl, 0, sizeof(int32_t) * 2) != hipSuccess) rc = QS_EDEVICE;
-    if (!rc && hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * R) != hipSuccess) rc = QS_EDEVICE;
-    if (!rc && hipMemset(b->sc.arrive, 0, sizeof(int32_t) * R) != hipSuccess) rc = QS_EDEVICE;
+    if (!rc && hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * R * qs_pipe_parts()) != hipSuccess)
+        rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.done, 0, sizeof(int32_t) * R) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.locks, 0, sizeof(int32_t) * b->sc.nslots) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.err, 0, sizeof(int32_t)) != hipSuccess) rc = QS_EDEVICE;
@@ -891,8 +883,7 @@ int qs_batch_synchronize(qs_batch *b) {
         // clear the flag and the pipelined kernel's counters so the next pick starts clean
         const int32_t zero = 0;
         (void)hipMemcpy(b->sc.err, &zero, sizeof zero, hipMemcpyHostToDevice);
-        (void)hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * b->max_rows);
-        (void)hipMemset(b->sc.arrive, 0, sizeof(int32_t) * b->max_rows);
+        (void)hipMemset(b->sc.rowmax, 0, sizeof(uint32_t) * b->max_rows * qs_pipe_parts());
         (void)hipMemset(b->sc.done, 0, sizeof(int32_t) * b->max_rows);
         (void)hipMemset(b->op.ctr, 0, sizeof(uint32_t) * b->max_rows * QS_OP_CTR_STRIDE);
         (void)hipMemset(b->op.ctl, 0, sizeof(int32_t) * 2);

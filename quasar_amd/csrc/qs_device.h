@@ -180,6 +180,30 @@ __device__ __forceinline__ uint32_t wave_kth(const uint32_t (&k)[Q], int K, int 
     return th;
 }
 
+// The same sort for 32-bit values.
+template <int SIZE, int S>
+__device__ __forceinline__ void bitonic_step_u32(uint32_t &v, int lane) {
+    const uint32_t o = xor_lane<S>(v);
+    const bool keep_max = ((lane & S) == 0) == ((lane & SIZE) == 0);
+    v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
+}
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
+    const int lane = threadIdx.x & 63;
+    bitonic_step_u32<2, 1>(v, lane);
+    bitonic_step_u32<4, 2>(v, lane);   bitonic_step_u32<4, 1>(v, lane);
+    bitonic_step_u32<8, 4>(v, lane);   bitonic_step_u32<8, 2>(v, lane);
+    bitonic_step_u32<8, 1>(v, lane);
+    bitonic_step_u32<16, 8>(v, lane);  bitonic_step_u32<16, 4>(v, lane);
+    bitonic_step_u32<16, 2>(v, lane);  bitonic_step_u32<16, 1>(v, lane);
+    bitonic_step_u32<32, 16>(v, lane); bitonic_step_u32<32, 8>(v, lane);
+    bitonic_step_u32<32, 4>(v, lane);  bitonic_step_u32<32, 2>(v, lane);
+    bitonic_step_u32<32, 1>(v, lane);
+    bitonic_step_u32<64, 32>(v, lane); bitonic_step_u32<64, 16>(v, lane);
+    bitonic_step_u32<64, 8>(v, lane);  bitonic_step_u32<64, 4>(v, lane);
+    bitonic_step_u32<64, 2>(v, lane);  bitonic_step_u32<64, 1>(v, lane);
+    return v;
+}
+
 // Inclusive prefix sum over the lanes.
 __device__ __forceinline__ double wave_scan_d(double v) {
     const int lane = threadIdx.x & 63;
@@ -293,8 +317,7 @@ struct Scratch {
     uint64_t *full_keys;  // [nslots][2][vocab]
     uint32_t *full_bm;    // [nslots][vocab/32+1]
     int32_t *err;         // [1] sticky error flag (bounded wait gave up)
-    uint32_t *rowmax;     // [rows] pipelined kernel: row max key, combined by atomicMax
-    int32_t *arrive;      // [rows] pipelined kernel: parts whose max is published
+    uint32_t *rowmax;     // [rows*parts] pipelined kernel: each part's max key (0: unpublished)
     int32_t *done;        // [rows] pipelined kernel: parts whose sums/candidates are written
     int nslots;
     int ccap;             // candidates per slice list

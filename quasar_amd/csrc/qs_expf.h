@@ -78,6 +78,47 @@ QS_EXPF_FN float qs_expf_core(float x, const uint64_t *tab) {
     return (float)y;
 }
 
+#ifdef __HIPCC__
+/* qs_expf_core on four arguments at once, in phases (argument reductions, then the four
+ * table reads, then the polynomials, then the scaling), so the table reads are in flight
+ * together instead of each waiting out its own latency.  Same operations, same results. */
+__device__ static inline void qs_expf4_core(const float (&x)[4], float (&e)[4],
+                                            const uint64_t *tab) {
+    double r[4];
+    uint32_t klo[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const double xd = (double)x[k];
+        double kd = __builtin_fma(QS_EXPF_INVLN2N, xd, QS_EXPF_SHIFT);
+        klo[k] = (uint32_t)qs_d2u(kd);
+        kd = kd - QS_EXPF_SHIFT;
+        r[k] = __builtin_fma(QS_EXPF_INVLN2N, xd, -kd);
+    }
+    uint64_t te[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) te[k] = tab[klo[k] & (QS_EXPF_TAB_N - 1)];
+    double y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const double z = __builtin_fma(QS_EXPF_C0, r[k], QS_EXPF_C1);
+        const double r2 = r[k] * r[k];
+        double t = __builtin_fma(QS_EXPF_C2, r[k], 1.0);
+        y[k] = __builtin_fma(z, r2, t);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t thi = (uint32_t)(te[k] >> 32);
+#ifdef __HIP_DEVICE_COMPILE__
+        asm("v_lshl_add_u32 %0, %1, 15, %0" : "+v"(thi) : "v"(klo[k]));
+#else
+        thi += klo[k] << 15;
+#endif
+        const double sc = qs_u2d(((uint64_t)thi << 32) | (uint32_t)te[k]);
+        e[k] = (float)(y[k] * sc);
+    }
+}
+#endif
+
 /* Full routine, including the |x| >= 88, infinity and NaN cases. */
 QS_EXPF_FN float qs_expf_tab(float x, const uint64_t *tab) {
     uint32_t top = (qs_f2u(x) >> 20) & 0x7ffu;

@@ -60,6 +60,7 @@ int qs_pipe_supported(int n_rows, int n_vocab, int64_t row_stride, const void *l
 // Dynamic LDS bytes of that kernel for a vocabulary width.
 size_t qs_pipe_lds_bytes(int n_vocab);
 // Rows are split in this many parts (the per-part scratch needs rows * parts entries).
+int qs_pipe_grid(int max_vocab);
 int qs_pipe_parts(void);
 // Cooperative launch of the pipelined pick on `stream`.
 int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vocab,

@@ -1,6 +1,7 @@
 // qs_pipe.hip - the pipelined pick for batches large enough to fill the GPU.
 //
-// One persistent workgroup of 1024 threads per CU (cooperative launch, grid G).  Every row
+// One persistent workgroup of 1024 threads per CU (grid G <= CUs, checked against the
+// device's occupancy for this kernel, so the whole grid is resident at once).  Every row
 // is cut into PARTS = 8 parts; at stage s the grid works on G/PARTS rows, part j of
 // row-in-stage q going to workgroup q + j*G/PARTS (with G a multiple of 64 the eight
 // workgroups of a row are congruent mod 8, i.e. on one XCD when workgroups are dealt to
@@ -29,8 +30,8 @@
 //
 // Every wait is bounded (SPIN_LIMIT polls): one that gives up sets the sticky error flag
 // and the pick reports an error instead of hanging.  A workgroup only waits for
-// publications that its partners make before they wait on anything later, and the
-// cooperative launch keeps every workgroup resident, so the waits end.
+// publications that its partners make before they wait on anything later, and every
+// workgroup of the grid is resident, so the waits end.
 
 #include <hip/hip_runtime.h>
 
@@ -54,9 +55,7 @@ constexpr int PARTS = 8;             // parts per row
 constexpr int UP = 5;                // float4 per data thread per part
 constexpr int PCAP = 512;            // candidates per part (<= Scratch::ccap)
 constexpr int FCAP = 4096;           // candidates gathered per row in the epilogue
-constexpr int TOPW_MAX = 16;         // thread maxima a data wave reports per part, at most
 constexpr int NDW = NWV - 1;         // data waves
-static_assert(TOPW_MAX * NDW <= 256, "the control wave holds the reports 4 per lane");
 
 __constant__ uint64_t c_exp_tab_p[QS_EXPF_TAB_N] = QS_EXPF_TABLE_INIT;
 
@@ -81,7 +80,6 @@ struct PartCfg {
     float rp;                        // repeat penalty
     int flags;                       // CFG_GREEDY | CFG_PEN
     int kw;                          // candidates the part keeps at least (part_k)
-    int tw;                          // thread maxima each data wave reports
 };
 constexpr int CFG_GREEDY = 1, CFG_PEN = 2;
 
@@ -90,7 +88,6 @@ struct PipeLds {
     DecideLds<NT> dl;
     // hand-offs between the data waves and the control wave, double-buffered by part
     // parity: written for one part while the other part's copy is read
-    float wmax[2][NWV];              // per-wave part max of a completed part
     float wbv[2][NWV];               // greedy: per-wave best value / index
     int wbi[2][NWV];
     double wsum[2][NWV];             // per-wave partial sums of a summed part
@@ -99,8 +96,7 @@ struct PipeLds {
     uint32_t maxkey[3];              // row max keys (by part index mod 3)
     uint32_t theta[4];               // candidate threshold keys (by part index mod 4)
     PartCfg cfg[4];                  // by part index mod 4
-    uint32_t wtop[2][TOPW_MAX * NDW];    // data waves' largest thread maxima (by parity;
-                                         // report i of wave w at i * NDW + w - 1)
+    uint32_t lmax[2][DT];            // each data thread's max key of a completed part
     RowTotals tot;
     int offs[PARTS + 1];
     float gbv;
@@ -134,36 +130,38 @@ __device__ __forceinline__ bool task_valid(const PipeArgs &a, int s, const Geo &
     return s < a.stages && task_row(s, w, g.rps) < a.n_rows;
 }
 
-// Control wave: the settings of `row` for the data waves.
-__device__ __forceinline__ void set_cfg(PartCfg &c, const PipeArgs &a, int row) {
+// Control wave: the settings of a row for the data waves (from its fetched parameters).
+__device__ __forceinline__ void set_cfg(PartCfg &c, const qs_row_param &P, bool pen) {
     if ((threadIdx.x & 63) != 0) return;
-    const qs_row_param P = a.st.prm[row];
-    const bool pen = P.repeat_penalty > 1.0f && a.st.hlen[row] > 0 && P.ring_cap > 0;
     c.inv_t = P.inv_t;
     c.rp = P.repeat_penalty;
     c.flags = (row_greedy(P) ? CFG_GREEDY : 0) | (pen ? CFG_PEN : 0);
     c.kw = part_k(P);
-    c.tw = min((c.kw + NDW - 1) / NDW + 1, TOPW_MAX);
 }
 
-// Data waves: loads of one part into registers (float4 c = c_lo + u*DT + dt; lanes past
-// the part read the part's last float4, and are masked later).  Every stage issues the
-// same UP loads, so each wave's memory counter names exactly the loads a use waits for;
-// a stage with no part (past the last row) reads row 0's first float4 in every lane.
+// Data waves: loads of one part into registers, through a buffer resource over the part
+// (base: its first float4; size: its length), float4 u of data thread dt at byte offset
+// (u*DT + dt)*16.  Loads past the part's end, and all loads of a stage without a part
+// (size 0), return zeros without a memory access.  Every stage issues the same UP loads,
+// so each wave's memory counter names exactly the loads a use waits for.
+constexpr int BUF_WORD3 = 0x00020000;    // raw buffer, 32-bit data format
 __device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a, int row,
                                             bool live, const Geo &g) {
-    const float4 *x4 = (const float4 *)(a.logits + (live ? (int64_t)row * a.stride : 0));
-    const int dt = data_tid();
+    const float *base = a.logits + (live ? (int64_t)row * a.stride + 4 * (int64_t)g.c_lo : 0);
+    const int bytes = live ? (g.c_hi - g.c_lo) * 16 : 0;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, bytes, BUF_WORD3);
+    const int off = data_tid() * 16;
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
-        const int c = g.c_lo + u * DT + dt;
-        buf[u] = x4[live ? (c < g.c_hi ? c : g.c_hi - 1) : 0];
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * DT * 16, 0, 0);
+        buf[u] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]),
+                             __uint_as_float(v[2]), __uint_as_float(v[3]));
     }
 }
 
-// Data waves: penalty (sample.c:118-128), per-wave part max (greedy: first argmax) and the
-// wave's cf.tw largest thread maxima (keys of cf.tw distinct logits), from which the
-// control wave takes the part's candidate threshold.
+// Data waves: penalty (sample.c:118-128) and each thread's max key (the control wave takes
+// the part's max and candidate threshold from them); greedy rows: the wave's first argmax.
 __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
                                               const uint32_t *bm, const PartCfg &cf,
                                               PipeLds &pl, int par) {
@@ -173,27 +171,27 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
     const bool greedy = (cf.flags & CFG_GREEDY) != 0;
     const float qnan = __builtin_nanf("");
     const int dt = data_tid();
+    // history bits of float4 u: word (u*DT + dt)/8 = u*DT/8 + dt/8, bits 4*(dt%8).. (DT is a
+    // multiple of 8, so the shift is the same for every u)
+    const uint32_t *bw = bm + (dt >> 3);
+    const uint32_t bsh = (uint32_t)(dt & 7) * 4u;
     float mx = -INFINITY, bv = -INFINITY;
     int bi = -1;
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
         const int c = g.c_lo + u * DT + dt;
         float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
-        if (c >= g.c_hi) w[0] = w[1] = w[2] = w[3] = qnan;
+        if (u == UP - 1 && c >= g.c_hi)             // past the part: only the last group
+            w[0] = w[1] = w[2] = w[3] = qnan;
         if (pen) {
-            uint32_t nib = 0u;
-            if (c < g.c_hi) {
-                const int r = 4 * c - g.lo;
-                nib = (bm[r >> 5] >> (r & 31)) & 0xFu;
-            }
+            const uint32_t nib = __builtin_amdgcn_ubfe(bw[u * (DT / 8)], bsh, 4);
             if (__ballot(nib != 0u)) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     if ((nib >> k) & 1u) w[k] = penalise(w[k], rp);
             }
         }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) mx = w[k] > mx ? w[k] : mx;
+        mx = fmaxf(mx, fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3])));   // NaN never wins
         if (greedy) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
@@ -201,22 +199,14 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
         }
         buf[u] = make_float4(w[0], w[1], w[2], w[3]);
     }
-    const float m = wave_max_f(mx);
     if (greedy) {
         wave_best(bv, bi);
-    } else {
-        uint32_t key = f2key(mx);
-        for (int i = 0; i < cf.tw; ++i) {
-            const uint32_t top = wave_max_u(key);
-            if (lane == 0) pl.wtop[par][i * NDW + wv - 1] = top;
-            const int at = __builtin_ctzll(__ballot(key == top));
-            if (lane == at) key = 0u;                  // each lane reports at most once
+        if (lane == 0) {
+            pl.wbv[par][wv] = bv;
+            pl.wbi[par][wv] = bi;
         }
-    }
-    if (lane == 0) {
-        pl.wmax[par][wv] = m;
-        pl.wbv[par][wv] = bv;
-        pl.wbi[par][wv] = bi;
+    } else {
+        pl.lmax[par][dt] = f2key(mx);
     }
 }
 
@@ -234,7 +224,9 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
     const float msc = key2f(maxkey) * inv_t;
     const float thr = msc - 30.0f;
     if ((cf.flags & CFG_GREEDY) || !isfinite(msc)) return;   // decided in the epilogue
-    const float thf = key2f(th);
+    // candidates: every w >= key2f(th), tested as w*inv_t >= key2f(th)*inv_t (monotone in
+    // w, so a superset; rejected logits stay below th)
+    const float ths = key2f(th) * inv_t;
     const uint64_t *tab = pl.dl.tab;
     float xo = X_OUT;
     asm volatile("" : "+v"(xo));                    // a register, selected before the exp
@@ -246,27 +238,38 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
         const int c = g.c_lo + u * DT + dt;
         const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
         float sc[4];
-        bool in[4];
+        uint64_t in[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             sc[k] = w[k] * inv_t;
-            in[k] = sc[k] >= thr;                   // NaN (masked or past the part) is out
-            cnt += __popcll(__ballot(in[k]));
+            in[k] = __ballot(sc[k] >= thr);         // NaN (masked or past the part) is out
+            cnt += __popcll(in[k]);
         }
-        if (__ballot(in[0] | in[1] | in[2] | in[3])) {
-            float e[4];
+        const uint64_t all = __ballot(true);
+        if ((in[0] & in[1] & in[2] & in[3]) == all) {   // every lane's four in the window
+            float xa[4], e[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) e[k] = qs_expf_core(in[k] ? sc[k] - msc : xo, tab);
+            for (int k = 0; k < 4; ++k) xa[k] = sc[k] - msc;
+            qs_expf4_core(xa, e, tab);
+            acc0 += (double)e[0];
+            acc1 += (double)e[1];
+            acc0 += (double)e[2];
+            acc1 += (double)e[3];
+        } else if (in[0] | in[1] | in[2] | in[3]) {
+            float xa[4], e[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xa[k] = sc[k] >= thr ? sc[k] - msc : xo;
+            qs_expf4_core(xa, e, tab);
             acc0 += (double)e[0];
             acc1 += (double)e[1];
             acc0 += (double)e[2];
             acc1 += (double)e[3];
         }
-        const float m4 = fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3]));
-        if (__ballot(m4 >= thf)) {
+        const float m4 = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        if (__ballot(m4 >= ths)) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                if (w[k] >= thf) {
+                if (sc[k] >= ths) {
                     const int pos = atomicAdd(&pl.ncand[par], 1);
                     if (pos < PCAP) {
                         ckey[pos] = f2key(w[k]);
@@ -283,99 +286,145 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
     }
 }
 
-// Control wave: wait (bounded) until all parts of `row` published their max; its key.
-// `first` is an arrival count read earlier (its latency overlapped other work).
-__device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row, int first = -1) {
+// Control wave: wait (bounded) until all parts of `row` published their max key (one slot
+// per part, 0 until published: keys of part maxima are never 0); the row max key.
+__device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row) {
     const int lane = threadIdx.x & 63;
-    uint32_t key = 0u;
-    if (lane == 0) {
-        int it = 0;
-        while ((first >= PARTS ? (first = PARTS) : (first = ld_dev(&a.sc.arrive[row]))) < PARTS) {
-            if (++it >= SPIN_LIMIT) {
-                atomicOr(a.sc.err, 2);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+    const uint32_t *slot = a.sc.rowmax + (int64_t)row * PARTS;
+    uint32_t k = 0u;
+    int it = 0;
+    while (true) {
+        k = lane < PARTS ? ld_dev(&slot[lane]) : 1u;
+        if (__ballot(k == 0u) == 0ull) break;
+        if (++it >= SPIN_LIMIT) {
+            if (lane == 0) atomicOr(a.sc.err, 2);
+            break;
         }
-        key = ld_dev(&a.sc.rowmax[row]);
+        __builtin_amdgcn_s_sleep(1);
     }
-    return __shfl(key, 0, 64);
+    return wave_max_u(lane < PARTS ? k : 0u);
 }
 
-// Control wave: the history ids of `row` (up to RING_PF per lane stay in registers, so
-// their loads overlap the control wave's other waits) and the bitmap they set.
+// Control wave: a row's parameters, history ring position and the first RING_PF*64 ring
+// slots, all loaded at once (the slots do not wait for the position: a slot p holds a
+// history id iff (p - head) mod cap < len, the positions sample.c:118 marks).  Fetched a
+// stage before the row's part is completed, so the loads complete during other work.
 constexpr int RING_PF = 8;
-struct RingIds {
-    int id[RING_PF];
-    int len, head, cap;
-    bool pen;
+struct RowFetch {
+    qs_row_param P;
+    int len, head;
+    int slot[RING_PF];
 };
-
-__device__ __forceinline__ RingIds ring_fetch(const PipeArgs &a, int row) {
+__device__ __forceinline__ RowFetch fetch_row(const PipeArgs &a, int row) {
     const int lane = threadIdx.x & 63;
-    RingIds r;
-    const RowState &st = a.st;
-    const qs_row_param P = st.prm[row];
-    r.len = st.hlen[row];
-    r.head = st.hhead[row];
-    r.cap = P.ring_cap;
-    r.pen = P.repeat_penalty > 1.0f && r.len > 0 && r.cap > 0;
-    const int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+    RowFetch f;
+    f.P = a.st.prm[row];
+    f.len = a.st.hlen[row];
+    f.head = a.st.hhead[row];
+    const int32_t *ring = a.st.ring + (int64_t)row * a.st.ring_stride;
 #pragma unroll
     for (int q = 0; q < RING_PF; ++q) {
-        const int j = q * 64 + lane;
-        r.id[q] = (r.pen && j < r.len) ? ring[(r.head + j) % r.cap] : -1;
+        const int p = q * 64 + lane;
+        f.slot[q] = p < a.st.ring_stride ? ring[p] : -1;
     }
-    return r;
+    return f;
+}
+__device__ __forceinline__ bool row_pen(const RowFetch &f) {
+    return f.P.repeat_penalty > 1.0f && f.len > 0 && f.P.ring_cap > 0;
 }
 
-__device__ __forceinline__ void bitmap_build(uint32_t *bm, const RingIds &r, const PipeArgs &a,
+// Control wave: the history bitmap of this workgroup's part of a row.
+__device__ __forceinline__ void bitmap_build(uint32_t *bm, const RowFetch &f, const PipeArgs &a,
                                              int row, const Geo &g) {
     const int lane = threadIdx.x & 63;
-    if (!r.pen) return;
+    if (!row_pen(f)) return;
     for (int j = lane; j < g.bm_words; j += 64) bm[j] = 0u;
-    const int hi = g.c_hi * 4;
+    const int hi = g.c_hi * 4, cap = f.P.ring_cap;
+    auto mark = [&](int p, int id) {
+        int d = p - f.head;
+        if (d < 0) d += cap;
+        if (p < cap && d < f.len && id >= g.lo && id < hi)
+            atomicOr(&bm[(id - g.lo) >> 5], 1u << ((id - g.lo) & 31));
+    };
 #pragma unroll
-    for (int q = 0; q < RING_PF; ++q) {
-        const int id = r.id[q];
-        if (id >= g.lo && id < hi) atomicOr(&bm[(id - g.lo) >> 5], 1u << ((id - g.lo) & 31));
-    }
-    if (r.len > RING_PF * 64) {                     // longer histories: the rest directly
+    for (int q = 0; q < RING_PF; ++q) mark(q * 64 + lane, f.slot[q]);
+    if (cap > RING_PF * 64) {                       // longer rings: the rest directly
         const int32_t *ring = a.st.ring + (int64_t)row * a.st.ring_stride;
-        for (int j = RING_PF * 64 + lane; j < r.len; j += 64) {
-            const int id = ring[(r.head + j) % r.cap];
-            if (id >= g.lo && id < hi) atomicOr(&bm[(id - g.lo) >> 5], 1u << ((id - g.lo) & 31));
-        }
+        for (int p = RING_PF * 64 + lane; p < cap; p += 64) mark(p, ring[p]);
     }
 }
 
-__device__ __forceinline__ void control_bitmap(uint32_t *bm, const PipeArgs &a, int row,
-                                               const Geo &g) {
-    const RingIds r = ring_fetch(a, row);
-    bitmap_build(bm, r, a, row, g);
+// Control wave: the largest of a part's thread max keys.
+__device__ __forceinline__ uint32_t part_max(const uint32_t *lm) {
+    const int lane = threadIdx.x & 63;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int j = 0; j < NDW; ++j) m = max(m, lm[j * 64 + lane]);
+    return wave_max_u(m);
 }
 
-// Control wave: the part's candidate threshold, the kw-th largest of the thread maxima the
-// data waves reported (kw distinct logits of the part reach it; the part keeps every logit
-// at or above it, and every other one lies below it).
-__device__ __forceinline__ uint32_t part_theta(const uint32_t *wtop, const PartCfg &cf) {
-    const int n = cf.tw * NDW;
+__device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
+    return max(min(a, b), min(max(a, b), c));
+}
+// (t1 >= t2 >= t3) keeps the three largest of itself and v.
+__device__ __forceinline__ void top3_insert(uint32_t &t1, uint32_t &t2, uint32_t &t3, uint32_t v) {
+    const uint32_t n1 = max(t1, v), n2 = umed3(t1, t2, v), n3 = umed3(t2, t3, v);
+    t1 = n1;
+    t2 = n2;
+    t3 = n3;
+}
+
+// Control wave: the part's candidate threshold, the kw-th largest of a set of thread max
+// keys (kw distinct logits of the part reach it; the part keeps every logit at or above
+// it, and every other one lies below it).  The set is each data wave's three largest
+// (lanes 4j..4j+3 keep the top three of data wave j's 64 keys, 16 each, then merge within
+// the quad), or, when kw exceeds those, all of them.
+__device__ __forceinline__ uint32_t part_theta(const uint32_t *lm, const PartCfg &cf) {
     const int lane = threadIdx.x & 63;
-    uint32_t k[4];
+    uint32_t th;
+    if (cf.kw <= 3 * NDW) {
+        const int j = lane >> 2;
+        uint32_t t1 = 0u, t2 = 0u, t3 = 0u;          // thread max keys are never 0
+        if (j < NDW) {
+            const uint32_t *src = lm + j * 64 + (lane & 3) * 16;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) k[q] = q * 64 + lane < n ? wtop[q * 64 + lane] : 0u;
-    const uint32_t th = wave_kth(k, cf.kw, n);
+            for (int i = 0; i < 16; ++i) top3_insert(t1, t2, t3, src[i]);
+        }
+        {
+            const uint32_t o1 = xor_lane<1>(t1), o2 = xor_lane<1>(t2), o3 = xor_lane<1>(t3);
+            top3_insert(t1, t2, t3, o1);
+            top3_insert(t1, t2, t3, o2);
+            top3_insert(t1, t2, t3, o3);
+        }
+        {
+            const uint32_t o1 = xor_lane<2>(t1), o2 = xor_lane<2>(t2), o3 = xor_lane<2>(t3);
+            top3_insert(t1, t2, t3, o1);
+            top3_insert(t1, t2, t3, o2);
+            top3_insert(t1, t2, t3, o3);
+        }
+        // the 45 values one per lane (lane 4j+q: wave j's (q+1)-th), sorted: the kw-th
+        const int q = lane & 3;
+        uint32_t v = (j < NDW && q < 3) ? (q == 0 ? t1 : q == 1 ? t2 : t3) : 0u;
+        v = wave_sort_desc_u32(v);
+        th = (uint32_t)__builtin_amdgcn_readlane((int)v, cf.kw - 1);
+    } else {
+        uint32_t k[NDW];
+#pragma unroll
+        for (int j = 0; j < NDW; ++j) k[j] = lm[j * 64 + lane];
+        th = wave_kth(k, cf.kw, DT);
+    }
     return th <= KEY_NEG_INF ? KEY_NEG_INF + 1u : th;   // -inf and NaN never qualify
 }
 
 // Control wave: publish the completed part's max (sampling) or best (greedy).
 __device__ __forceinline__ void control_publish(const PipeArgs &a, int row, const Geo &g,
-                                                PipeLds &pl, int par) {
+                                                PipeLds &pl, int par, int cfg_slot) {
     const int lane = threadIdx.x & 63;
+    const bool greedy = (pl.cfg[cfg_slot].flags & CFG_GREEDY) != 0;
+    const uint32_t mk = greedy ? 0u : part_max(pl.lmax[par]);
     if (lane != 0) return;
-    const qs_row_param P = a.st.prm[row];
     const int li = row * PARTS + g.part;
-    if (row_greedy(P)) {
+    if (greedy) {
         float v0 = pl.wbv[par][1];
         int i0 = pl.wbi[par][1];
         for (int k = 2; k < NWV; ++k) best_combine(v0, i0, pl.wbv[par][k], pl.wbi[par][k]);
@@ -385,23 +434,19 @@ __device__ __forceinline__ void control_publish(const PipeArgs &a, int row, cons
         add_dev(&a.sc.done[row], 1);
         return;
     }
-    float t = pl.wmax[par][1];
-    for (int k = 2; k < NWV; ++k) t = fmaxf(t, pl.wmax[par][k]);
-    __hip_atomic_fetch_max(&a.sc.rowmax[row], f2key(t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    stores_done();
-    add_dev(&a.sc.arrive[row], 1);
+    st_dev(&a.sc.rowmax[li], mk);                 // seen by the partners' polls
 }
 
-// Control wave: store a summed part's results and release them.
-__device__ __forceinline__ void control_store(const PipeArgs &a, int row, const Geo &g,
+// Control wave: store a summed part's results; control_release announces them once every
+// store has completed.  Returns whether there is anything to announce.
+__device__ __forceinline__ bool control_store(const PipeArgs &a, int row, const Geo &g,
                                               uint32_t maxkey, uint32_t th,
                                               const uint32_t *ckey, const int32_t *cid,
-                                              PipeLds &pl, int par) {
+                                              const PartCfg &cf, PipeLds &pl, int par) {
     const int lane = threadIdx.x & 63;
-    const qs_row_param P = a.st.prm[row];
-    if (row_greedy(P)) return;                    // published with its best already
+    if (cf.flags & CFG_GREEDY) return false;      // published with its best already
     const int li = row * PARTS + g.part;
-    const bool live = isfinite(key2f(maxkey) * P.inv_t);
+    const bool live = isfinite(key2f(maxkey) * cf.inv_t);
     const int nc = pl.ncand[par];
     const int n = live ? min(nc, PCAP) : 0;
     const int ovf = live && nc > PCAP;
@@ -425,11 +470,12 @@ __device__ __forceinline__ void control_store(const PipeArgs &a, int row, const 
         st_dev(&a.sc.cflag[li], ovf);
         st_dev(&a.sc.crej[li], (live && th > KEY_NEG_INF) ? th - 1u : 0u);
     }
+    if (lane == 0) pl.ncand[par] = 0;
+    return true;
+}
+__device__ __forceinline__ void control_release(const PipeArgs &a, int row) {
     stores_done();                                // the whole wave's stores, then the count
-    if (lane == 0) {
-        add_dev(&a.sc.done[row], 1);
-        pl.ncand[par] = 0;
-    }
+    if ((threadIdx.x & 63) == 0) add_dev(&a.sc.done[row], 1);
 }
 
 // Finish row r: gather its PARTS partial results and decide (all threads).
@@ -468,6 +514,7 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
             pc = wave_sum_i(pc);
             cf = wave_or_i(cf);
             cr = wave_max_u(cr);
+            const uint32_t rmx = wave_max_u(have ? ld_dev(&sc.rowmax[(int64_t)row * PARTS + lane]) : 0u);
             int incl = cc;
             for (int o = 1; o < 64; o <<= 1) {
                 const int t = __shfl_up(incl, o, 64);
@@ -476,7 +523,7 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
             if (have) pl.offs[lane] = incl - cc;
             if (lane == 63) pl.offs[PARTS] = incl;
             if (lane == 0) {
-                pl.tot.maxl = key2f(ld_dev(&sc.rowmax[row]));
+                pl.tot.maxl = key2f(rmx);
                 pl.tot.sum = ps;
                 pl.tot.nwin = pc;
                 pl.tot.cflag = cf;
@@ -527,11 +574,8 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
                             a.out, a.diag, slot);
     }
     __syncthreads();
-    if (tid == 0) {                               // ready for the next pick
-        st_dev(&sc.arrive[row], 0);
-        st_dev(&sc.done[row], 0);
-        st_dev(&sc.rowmax[row], 0u);
-    }
+    if (tid < PARTS) st_dev(&sc.rowmax[(int64_t)row * PARTS + tid], 0u);   // ready for the
+    if (tid == 0) st_dev(&sc.done[row], 0);                                 // next pick
 }
 
 // One stage, data waves: sum part s (in `cur`), issue the loads of part s+3 into `cur`,
@@ -557,7 +601,8 @@ __device__ __forceinline__ void data_stage(float4 (&cur)[UP], float4 (&ld)[UP], 
 // row max.  Every hand-off crosses the barrier at the top of a stage into a slot the other
 // side does not use in that stage (parity for bitmaps, wave results and candidate lists;
 // part index mod 3 for row maxima, mod 4 for thresholds).
-__device__ __forceinline__ void control_stage(int s, const PipeArgs &a, const Geo &g, int w,
+__device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArgs &a,
+                                              const Geo &g, int w,
                                               uint32_t *bm, const uint32_t *ckey,
                                               const int32_t *cid, PipeLds &pl) {
     const int lane = threadIdx.x & 63;
@@ -565,21 +610,25 @@ __device__ __forceinline__ void control_stage(int s, const PipeArgs &a, const Ge
     const int r1 = task_row(s + 1, w, g.rps), r3 = task_row(s + 3, w, g.rps);
     const int p1 = (s & 1) ^ 1;
     __syncthreads();
-    RingIds ring3;                               // in flight while publishing and storing
-    if (v3) {
-        ring3 = ring_fetch(a, r3);
-        set_cfg(pl.cfg[(s + 3) & 3], a, r3);
-    }
-    if (v1) control_publish(a, r1, g, pl, p1);
-    if (s >= 1 && task_valid(a, s - 1, g, w))
-        control_store(a, task_row(s - 1, w, g.rps), g, pl.maxkey[(s + 2) % 3],
-                      pl.theta[(s + 3) & 3], ckey + p1 * PCAP, cid + p1 * PCAP, pl, p1);
+    const RowFetch f3 = rp;                      // part s+3's row, fetched last stage
+    if (task_valid(a, s + 4, g, w)) rp = fetch_row(a, task_row(s + 4, w, g.rps));
+    if (v1) control_publish(a, r1, g, pl, p1, (s + 1) & 3);
+    const bool sv = s >= 1 && task_valid(a, s - 1, g, w);
+    const int rs = task_row(s - 1, w, g.rps);
+    bool rel = false;
+    if (sv)
+        rel = control_store(a, rs, g, pl.maxkey[(s + 2) % 3], pl.theta[(s + 3) & 3],
+                            ckey + p1 * PCAP, cid + p1 * PCAP, pl.cfg[(s + 3) & 3], pl, p1);
     if (v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY)) {
-        const uint32_t th = part_theta(pl.wtop[p1], pl.cfg[(s + 1) & 3]);
+        const uint32_t th = part_theta(pl.lmax[p1], pl.cfg[(s + 1) & 3]);
         if (lane == 0) pl.theta[(s + 1) & 3] = th;
     }
-    if (v3) bitmap_build(bm + p1 * g.bm_words, ring3, a, r3, g);
-    if (v1 && !row_greedy(a.st.prm[r1])) {
+    if (v3) {
+        bitmap_build(bm + p1 * g.bm_words, f3, a, r3, g);
+        set_cfg(pl.cfg[(s + 3) & 3], f3.P, row_pen(f3));   // part s-1's settings are used
+    }
+    if (rel) control_release(a, rs);
+    if (v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY)) {
         const uint32_t key = poll_rowmax(a, r1);
         if (lane == 0) pl.maxkey[(s + 1) % 3] = key;
     }
@@ -613,6 +662,7 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (wave != 0) {
         float4 B0[UP], B1[UP], B2[UP];
+        __syncthreads();                         // the control wave's fetches go first
         issue_loads(B0, a, r0, t0, g);
         issue_loads(B1, a, r1, t1, g);
         __syncthreads();
@@ -632,38 +682,48 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         // the control wave's steps are on every stage's critical path: it issues ahead of
         // the data wavefronts that share its SIMD
         __builtin_amdgcn_s_setprio(3);
+        // every row fetch of the prologue in flight before the data waves issue theirs
+        const bool t3 = task_valid(a, 3, g, w);
+        RowFetch f0, f1, f2, rp;
+        if (t0) f0 = fetch_row(a, r0);
+        if (t1) f1 = fetch_row(a, r1);
+        if (t2) f2 = fetch_row(a, r2);
+        if (t3) rp = fetch_row(a, task_row(3, w, g.rps));
+        __syncthreads();
         if (t0) {
-            set_cfg(pl.cfg[0], a, r0);
-            control_bitmap(bm, a, r0, g);
+            bitmap_build(bm, f0, a, r0, g);
+            set_cfg(pl.cfg[0], f0.P, row_pen(f0));
         }
         if (t1) {
-            set_cfg(pl.cfg[1], a, r1);
-            control_bitmap(bm + g.bm_words, a, r1, g);
+            bitmap_build(bm + g.bm_words, f1, a, r1, g);
+            set_cfg(pl.cfg[1], f1.P, row_pen(f1));
         }
         __syncthreads();
         __syncthreads();
-        if (t0) control_publish(a, r0, g, pl, 0);
+        if (t0) control_publish(a, r0, g, pl, 0, 0);
         if (t0 && !(pl.cfg[0].flags & CFG_GREEDY)) {
-            const uint32_t th = part_theta(pl.wtop[0], pl.cfg[0]);
+            const uint32_t th = part_theta(pl.lmax[0], pl.cfg[0]);
             if ((tid & 63) == 0) pl.theta[0] = th;
         }
         if (t2) {
-            set_cfg(pl.cfg[2], a, r2);
-            control_bitmap(bm, a, r2, g);
+            bitmap_build(bm, f2, a, r2, g);
+            set_cfg(pl.cfg[2], f2.P, row_pen(f2));
         }
-        if (t0 && !row_greedy(a.st.prm[r0])) {
+        if (t0 && !(pl.cfg[0].flags & CFG_GREEDY)) {
             const uint32_t key = poll_rowmax(a, r0);
             if ((tid & 63) == 0) pl.maxkey[0] = key;
         }
-        for (int s = 0; s < a.stages; ++s) control_stage(s, a, g, w, bm, ckey, cid, pl);
+        for (int s = 0; s < a.stages; ++s) control_stage(s, rp, a, g, w, bm, ckey, cid, pl);
     }
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     {                                                // the last summed part
         const int s = a.stages - 1;
         if (!data && s >= 0 && task_valid(a, s, g, w))
-            control_store(a, task_row(s, w, g.rps), g, pl.maxkey[s % 3], pl.theta[s & 3],
-                          ckey + (s & 1) * PCAP, cid + (s & 1) * PCAP, pl, s & 1);
+            if (control_store(a, task_row(s, w, g.rps), g, pl.maxkey[s % 3], pl.theta[s & 3],
+                              ckey + (s & 1) * PCAP, cid + (s & 1) * PCAP, pl.cfg[s & 3], pl,
+                              s & 1))
+                control_release(a, task_row(s, w, g.rps));
     }
     __syncthreads();
     // epilogue: rows r = w (mod G), each with this workgroup's full-window slot
@@ -678,6 +738,8 @@ int qs_pipe_supported(int n_rows, int n_vocab, int64_t row_stride, const void *l
     if (n_vocab % 4 != 0 || row_stride % 4 != 0 || ((uintptr_t)logits % 16) != 0) return 0;
     const int part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
     if (part_len > 4 * DT * UP || part_len < 4 * DT * (UP - 1)) return 0;
+    // the last part (possibly shorter) ends inside its last group of float4s too
+    if (n_vocab - (PARTS - 1) * part_len <= 4 * DT * (UP - 1)) return 0;
     if ((int64_t)n_rows * PARTS < grid) return 0;     // too few rows to fill the grid
     return 1;
 }
@@ -692,6 +754,21 @@ size_t qs_pipe_lds_bytes(int n_vocab) {
 }
 
 int qs_pipe_parts(void) { return PARTS; }
+
+// Workgroups of the pipelined kernel: a multiple of PARTS, at most one per CU, and only if
+// the device holds one workgroup per CU with the LDS the largest vocabulary needs (the
+// whole grid is then resident at once, so every workgroup's partners run); 0 otherwise.
+int qs_pipe_grid(int max_vocab) {
+    int dev = 0, ncu = 0, nb = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_pipe, NT, qs_pipe_lds_bytes(max_vocab)) !=
+            hipSuccess ||
+        nb < 1)
+        return 0;
+    return ncu / PARTS * PARTS;
+}
 
 int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vocab,
                    const RowState &st, const Scratch &sc, int32_t *out, qs_pick_diag *diag,
@@ -708,11 +785,10 @@ int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vo
     a.sc = sc;
     a.out = out;
     a.diag = diag;
-    void *args[] = {&a};
-    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_pipe, dim3(grid), dim3(NT),
-                                                    args, qs_pipe_lds_bytes(n_vocab), stream);
+    hipLaunchKernelGGL(k_pipe, dim3(grid), dim3(NT), qs_pipe_lds_bytes(n_vocab), stream, a);
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
-        qs_set_error("k_pipe cooperative launch: %s", hipGetErrorString(e));
+        qs_set_error("k_pipe launch: %s", hipGetErrorString(e));
         return e == hipErrorOutOfMemory ? QS_ENOMEM : QS_EDEVICE;
     }
     return 0;
