@@ -123,10 +123,11 @@ int qs_batch_set_history(qs_batch *b, int row0, int n_rows, const int32_t *ids,
 int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
                   int n_vocab, int32_t *d_out, qs_pick_diag *d_diag);
 
-/* Which kernels qs_batch_pick uses.  AUTO (the default) takes the split-row kernels.
- * SPLIT: three kernels per pick, the logits streamed twice.  PIPELINED: the persistent
- * pipelined kernel (at least one row per 4 CUs, vocabulary a multiple of 4 up to
- * 153,600, 16-byte aligned rows).  ONEPASS: the one-pass kernel, every logit read once
+/* Which kernels qs_batch_pick uses.  AUTO (the default) takes the pipelined kernel when
+ * it supports the pick and the split-row kernels otherwise.  SPLIT: three kernels per
+ * pick, the logits streamed twice.  PIPELINED: one persistent kernel, every logit read
+ * once (at least one row per 8 CUs; vocabulary a multiple of 4 from about 123,000 to
+ * 153,600; 16-byte aligned rows).  ONEPASS: the one-pass kernel, every logit read once
  * (vocabularies up to 655,360).  QUEUE: one persistent kernel over a queue of scan and
  * sum tasks (vocabularies up to 655,360).  A mode that does not support a pick returns
  * QS_EINVAL.  The results are identical; the modes exist for testing and measurement. */

@@ -823,7 +823,7 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
         return qs_onepass_launch(d_logits, row_stride, n_rows, n_vocab, kmax, st0, b->sc, b->op,
                                  d_out, d_diag, b->op_grid, b->stream);
     }
-    if (b->mode == QS_MODE_PIPELINED) {
+    if (b->mode == QS_MODE_PIPELINED || (b->mode == QS_MODE_AUTO && pipe_ok)) {
         return qs_pipe_launch(d_logits, row_stride, n_rows, n_vocab, st0, b->sc, d_out, d_diag,
                               b->pipe_grid, b->stream);
     }
