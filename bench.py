@@ -14,11 +14,16 @@ input (--buffers, default: more than 512 MiB in total) that each pick reads from
 
 Also reported on the same JSON line:
   roofline      algorithmic bytes per step (4V logits + 4H history + 4 id + 16 RNG per
-                row) over the measured step time, against 8 TB/s HBM
+                row) over the measured step time, against 8 TB/s HBM; `traffic` is the HBM
+                bytes per pick that hardware counters measured for the same workload and
+                kernels (profiles/traffic.json, written from rocprofv3 FETCH_SIZE and
+                WRITE_SIZE runs scaled by the same counters on a copy of known size; null
+                when no such measurement is committed)
   cpu_baseline  the reference's own sample.c (oracle/_ref, when built) or the CPU
                 restatement, on this host's cores, over a bounded sample of the same rows
   parity        the first step's ids against the CPU on every sampled row
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--mode M]
+       python bench.py --calibrate-copy [--copy-mib N]   (copies of N MiB, for the counters)
 """
 import argparse
 import json
@@ -51,7 +56,37 @@ def parse():
                          "twice the last-level cache)")
     ap.add_argument("--mode", choices=["auto", "split", "pipelined", "onepass", "queue"], default="auto",
                     help="which kernels a pick uses (qs_batch_set_mode)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run plain device copies of --copy-mib MiB (counter calibration)")
+    ap.add_argument("--copy-mib", type=int, default=512)
     return ap.parse_args()
+
+
+KERNELS = {"split": "k_scan + k_expsum + k_finalize", "pipelined": "k_pipe",
+           "onepass": "k_onepass", "queue": "k_queue"}
+MODE_NAMES = {1: "split", 2: "pipelined", 3: "onepass", 4: "queue"}
+
+
+def calibrate_copy(args):
+    """Plain copies of known size: their FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
+    counters that measure a pick's HBM traffic."""
+    import quasar_amd as qa
+    n = args.copy_mib << 20
+    src, dst = qa.DeviceBuffer(n), qa.DeviceBuffer(n)
+    qa.copy_device(dst, src, n, 4)
+    print(json.dumps({"calibrate_copy": {"bytes_read": n, "bytes_written": n, "copies": 4}}),
+          flush=True)
+
+
+def committed_traffic(workload, mode):
+    """HBM bytes per pick measured by counters for this workload and kernel, if committed."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f).get(f"{workload}/{mode}")
+    except (OSError, ValueError):
+        return None
+    return t
 
 
 def cpu_baseline(w, logits_host, hist, seeds, gpu_ids, args):
@@ -91,6 +126,8 @@ def main():
               "rows are independent, so a multi-GPU run is B/G rows per GPU with no "
               "exchange; run it per GPU.", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        return calibrate_copy(args)
     import quasar_amd as qa
     from quasar_amd.workloads import BENCH_WORKLOAD, STRESS, WORKLOADS
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -121,6 +158,7 @@ def main():
     if hist is not None:
         batch.set_history(0, hist)
 
+    used = MODE_NAMES.get(batch.resolve_mode(logits.ptr, V, B, V), "split")
     first_ids, diag = batch.pick(logits.ptr, V, B, V, diag=True)
     paths = {}
     for d in diag:
@@ -147,6 +185,7 @@ def main():
     rows_per_s = B / (ms_per_step * 1e-3)
     alg_bytes = B * w.algorithmic_bytes_per_row()
     achieved = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    traffic = committed_traffic(w.name, used)
     out = {
         "metric": METRIC,
         "value": rows_per_s,
@@ -163,14 +202,13 @@ def main():
         "config": {"workload": w.name, "batch": B, "vocab": V, "history": w.hist_len,
                    "temperature": w.temperature, "top_k": w.top_k, "top_p": w.top_p,
                    "min_p": w.min_p, "repeat_penalty": w.repeat_penalty,
-                   "mode": args.mode, "input_buffers": n_buf,
+                   "mode": args.mode, "kernels": used, "input_buffers": n_buf,
                    "input_bytes_total": n_buf * nbytes, "description": w.description},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": {"pipelined": "one pick (k_pipe)",
-                                "onepass": "one pick (k_onepass)",
-                                "queue": "one pick (k_queue)"}.get(
-                                    args.mode, "one pick (k_scan + k_expsum + k_finalize)"),
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
+                     "kernel": f"one pick ({KERNELS[used]})",
                      "bytes_per_step": alg_bytes},
         "cpu_baseline": cpu,
         "parity": parity,

@@ -134,6 +134,10 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
 enum { QS_MODE_AUTO = 0, QS_MODE_SPLIT = 1, QS_MODE_PIPELINED = 2, QS_MODE_ONEPASS = 3,
        QS_MODE_QUEUE = 4 };
 int qs_batch_set_mode(qs_batch *b, int mode);
+/* The QS_MODE_* (SPLIT, PIPELINED, ONEPASS or QUEUE) a qs_batch_pick with these arguments
+ * and the rows' current settings would use; QS_EINVAL for arguments it would reject. */
+int qs_batch_resolve_mode(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
+                          int n_vocab);
 
 /* Set one row's generator state and history exactly (oldest first), e.g. to carry a
  * sampler's state into a larger batch. */
@@ -170,6 +174,11 @@ int   qs_device_info(char *name, int name_cap, size_t *total_mem, int *n_cu);
  * the same generator. */
 int qs_gen_logits_device(float *d_out, int64_t row_stride, int64_t row0, int n_rows,
                          int n_vocab, int dist, float sigma, float boost, uint64_t seed);
+
+/* `iters` plain streaming copies of `bytes` (a multiple of 16, 16-byte aligned) from
+ * d_src to d_dst, then a device synchronization: a kernel of known memory traffic for
+ * calibrating hardware memory counters. */
+int qs_copy_device(void *d_dst, const void *d_src, size_t bytes, int iters);
 
 /* y[i] = the library's expf(x[i]) on the device, i < n (the softmax numerator routine,
  * exposed so tests can compare it with the host C library's expf). */

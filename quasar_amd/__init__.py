@@ -70,6 +70,12 @@ def gen_logits_device(buf, row_stride, row0, n_rows, n_vocab, dist, sigma, boost
           "qs_gen_logits_device")
 
 
+def copy_device(dst, src, nbytes, iters=1):
+    """`iters` plain streaming copies of nbytes from src to dst (DeviceBuffers): a kernel of
+    known memory traffic for calibrating hardware counters."""
+    check(load().qs_copy_device(dst.ptr, src.ptr, nbytes, iters), "qs_copy_device")
+
+
 def device_info():
     name = C.create_string_buffer(256)
     mem = C.c_size_t(0)
@@ -146,6 +152,12 @@ class Batch:
         """0: automatic, 1: split-row kernels, 2: pipelined kernel, 3: one-pass kernel,
         4: queue kernel (see quasar_sampler.h)."""
         check(self._lib.qs_batch_set_mode(self._b, int(mode)), "qs_batch_set_mode")
+
+    def resolve_mode(self, logits_ptr, row_stride, n_rows, n_vocab):
+        """The mode (MODE_SPLIT, MODE_PIPELINED, ...) a pick with these arguments uses."""
+        m = self._lib.qs_batch_resolve_mode(self._b, logits_ptr, row_stride, n_rows, n_vocab)
+        check(m if m < 0 else 0, "qs_batch_resolve_mode")
+        return m
 
     def set_history(self, row0, ids):
         ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))

@@ -40,6 +40,7 @@ PROTOS = [
     ("qs_batch_pick", _i, [_vp, _vp, _i64, _i, _i, _vp, _vp]),
     ("qs_batch_set_state", _i, [_vp, _i, _u64, C.POINTER(C.c_int32), _i]),
     ("qs_batch_set_mode", _i, [_vp, _i]),
+    ("qs_batch_resolve_mode", _i, [_vp, _vp, _i64, _i, _i]),
     ("qs_batch_synchronize", _i, [_vp]),
     ("qs_batch_get_state", _i, [_vp, _i, C.POINTER(C.c_uint64), C.POINTER(C.c_int32), _i,
                                 C.POINTER(C.c_int)]),
@@ -55,6 +56,7 @@ PROTOS = [
     ("qs_batch_time_picks", _i, [_vp, C.POINTER(_vp), _i, _i64, _i, _i, _vp, _i,
                                  C.POINTER(C.c_float)]),
     ("qs_expf_device", _i, [_vp, _vp, _i64]),
+    ("qs_copy_device", _i, [_vp, _vp, _sz, _i]),
 ]
 
 _lib = None

@@ -484,6 +484,12 @@ __global__ void __launch_bounds__(WG) k_gen(float *out, int64_t stride, int64_t 
     out[r * stride + c] = qs_gen_logit(&spec, (uint64_t)(row0 + r), c, vocab);
 }
 
+// A plain streaming copy (16-byte loads and stores), for calibrating memory counters.
+__global__ void __launch_bounds__(WG) k_copy(const float4 *x, float4 *y, int64_t n4) {
+    for (int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x; i < n4; i += (int64_t)gridDim.x * WG)
+        y[i] = x[i];
+}
+
 __global__ void __launch_bounds__(WG) k_expf(const float *x, float *y, int64_t n) {
     __shared__ uint64_t tab[QS_EXPF_TAB_N];
     if (threadIdx.x < QS_EXPF_TAB_N) tab[threadIdx.x] = c_exp_tab[threadIdx.x];
@@ -779,6 +785,44 @@ int qs_batch_get_state(qs_batch *b, int row, uint64_t *rng, int32_t *hist, int c
     return 0;
 }
 
+// The largest top-k among the sampling rows of [0, n_rows) and whether any row samples;
+// QS_EINVAL when a row's ring is larger than the batch holds.
+static int batch_kmax(const qs_batch *b, int n_rows, int *kmax, bool *any_sample) {
+    *kmax = 1;
+    *any_sample = false;
+    for (int r = 0; r < n_rows; ++r) {
+        const qs_row_param &p = b->h_prm[r];
+        if (row_greedy(p)) continue;
+        *any_sample = true;
+        const int k = row_ksel(p);
+        if (k > *kmax) *kmax = k;
+        if (p.ring_cap > b->max_last_n) { qs_set_error("ring capacity"); return QS_EINVAL; }
+    }
+    return 0;
+}
+
+static bool pipe_fits(const qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
+                      int n_vocab, int kmax) {
+    return b->pipe_grid > 0 && kmax <= K_MAX &&
+           qs_pipe_supported(n_rows, n_vocab, row_stride, d_logits, b->pipe_grid);
+}
+
+int qs_batch_resolve_mode(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
+                          int n_vocab) {
+    if (!b || n_rows < 1 || n_rows > b->max_rows || n_vocab < 1 || n_vocab > b->max_vocab ||
+        row_stride < n_vocab) {
+        qs_set_error("qs_batch_resolve_mode: bad arguments");
+        return QS_EINVAL;
+    }
+    if (b->mode != QS_MODE_AUTO) return b->mode;
+    int kmax = 1;
+    bool any = false;
+    const int rc = batch_kmax(b, n_rows, &kmax, &any);
+    if (rc) return rc;
+    return pipe_fits(b, d_logits, row_stride, n_rows, n_vocab, kmax) ? QS_MODE_PIPELINED
+                                                                     : QS_MODE_SPLIT;
+}
+
 int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
                   int n_vocab, int32_t *d_out, qs_pick_diag *d_diag) {
     if (!b || !d_logits || !d_out) { qs_set_error("qs_batch_pick: null argument"); return QS_EINVAL; }
@@ -790,18 +834,10 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
     }
     int kmax = 1;
     bool any_sample = false;
-    for (int r = 0; r < n_rows; ++r) {
-        const qs_row_param &p = b->h_prm[r];
-        if (row_greedy(p)) continue;
-        any_sample = true;
-        const int k = row_ksel(p);
-        if (k > kmax) kmax = k;
-        if (p.ring_cap > b->max_last_n) { qs_set_error("ring capacity"); return QS_EINVAL; }
-    }
+    if (const int rc = batch_kmax(b, n_rows, &kmax, &any_sample)) return rc;
     RowState st0{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
                  b->max_last_n > 0 ? b->max_last_n : 1};
-    const bool pipe_ok = b->pipe_grid > 0 && kmax <= K_MAX &&
-                         qs_pipe_supported(n_rows, n_vocab, row_stride, d_logits, b->pipe_grid);
+    const bool pipe_ok = pipe_fits(b, d_logits, row_stride, n_rows, n_vocab, kmax);
     if (b->mode == QS_MODE_PIPELINED && !pipe_ok) {
         qs_set_error("qs_batch_pick: the pipelined kernel does not support this pick");
         return QS_EINVAL;
@@ -969,6 +1005,26 @@ int qs_gen_logits_device(float *d_out, int64_t row_stride, int64_t row0, int n_r
                        n_rows, n_vocab, spec);
     HIP_TRY(hipGetLastError(), "k_gen launch");
     HIP_TRY(hipDeviceSynchronize(), "k_gen");
+    return 0;
+}
+
+int qs_copy_device(void *d_dst, const void *d_src, size_t bytes, int iters) {
+    if (!d_dst || !d_src || bytes % 16 != 0 || bytes == 0 || iters < 1 ||
+        (uintptr_t)d_dst % 16 != 0 || (uintptr_t)d_src % 16 != 0) {
+        qs_set_error("qs_copy_device: bad arguments");
+        return QS_EINVAL;
+    }
+    int dev = 0, ncu = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    HIP_TRY(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev), "CUs");
+    const int64_t n4 = (int64_t)(bytes / 16);
+    int64_t blocks = (n4 + WG - 1) / WG;
+    if (blocks > (int64_t)ncu * 16) blocks = (int64_t)ncu * 16;
+    for (int i = 0; i < iters; ++i)
+        hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(WG), 0, 0,
+                           (const float4 *)d_src, (float4 *)d_dst, n4);
+    HIP_TRY(hipGetLastError(), "k_copy launch");
+    HIP_TRY(hipDeviceSynchronize(), "k_copy");
     return 0;
 }
 
