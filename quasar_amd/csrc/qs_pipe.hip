@@ -177,6 +177,9 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
     const uint32_t bsh = (uint32_t)(dt & 7) * 4u;
     float mx = -INFINITY, bv = -INFINITY;
     int bi = -1;
+    uint32_t hw[UP];                                 // every history word read at once
+#pragma unroll
+    for (int u = 0; u < UP; ++u) hw[u] = pen ? bw[u * (DT / 8)] : 0u;
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
         const int c = g.c_lo + u * DT + dt;
@@ -184,7 +187,7 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
         if (u == UP - 1 && c >= g.c_hi)             // past the part: only the last group
             w[0] = w[1] = w[2] = w[3] = qnan;
         if (pen) {
-            const uint32_t nib = __builtin_amdgcn_ubfe(bw[u * (DT / 8)], bsh, 4);
+            const uint32_t nib = __builtin_amdgcn_ubfe(hw[u], bsh, 4);
             if (__ballot(nib != 0u)) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
@@ -265,8 +268,8 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
             acc0 += (double)e[2];
             acc1 += (double)e[3];
         }
-        const float m4 = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        if (__ballot(m4 >= ths)) {
+        if (__ballot(sc[0] >= ths) | __ballot(sc[1] >= ths) | __ballot(sc[2] >= ths) |
+            __ballot(sc[3] >= ths)) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 if (sc[k] >= ths) {
@@ -593,14 +596,15 @@ __device__ __forceinline__ void data_stage(float4 (&cur)[UP], float4 (&ld)[UP], 
         sum_part(cur, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
                  pl.theta[s & 3], pl, p0);
     issue_loads(cur, a, r3, v3, g);
-    if (v2) complete_part(ld, g, bm + p0 * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
+    if (v2) complete_part(ld, g, bm + ((s + 2) % 3) * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
 }
 
 // One stage, control wave: publish part s+1's max (completed during the previous stage),
 // store part s-1's sums and candidates, build part s+3's history bitmap, read part s+1's
 // row max.  Every hand-off crosses the barrier at the top of a stage into a slot the other
-// side does not use in that stage (parity for bitmaps, wave results and candidate lists;
-// part index mod 3 for row maxima, mod 4 for thresholds).
+// side does not use in that stage (part parity for thread maxima, wave results and
+// candidate lists; part index mod 3 for bitmaps and row maxima, mod 4 for thresholds and
+// settings).
 __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArgs &a,
                                               const Geo &g, int w,
                                               uint32_t *bm, const uint32_t *ckey,
@@ -624,7 +628,7 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
         if (lane == 0) pl.theta[(s + 1) & 3] = th;
     }
     if (v3) {
-        bitmap_build(bm + p1 * g.bm_words, f3, a, r3, g);
+        bitmap_build(bm + (s % 3) * g.bm_words, f3, a, r3, g);   // part s+3's slot
         set_cfg(pl.cfg[(s + 3) & 3], f3.P, row_pen(f3));   // part s-1's settings are used
     }
     if (rel) control_release(a, rs);
@@ -647,14 +651,14 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     g.c_lo = g.lo >> 2;
     g.c_hi = p_hi >> 2;
     g.bm_words = a.part_len / 32 + 1;
-    uint32_t *bm = dyn;                              // [2][bm_words]
-    uint32_t *ckey = dyn + 2 * g.bm_words;           // [2][PCAP]
+    uint32_t *bm = dyn;                              // [3][bm_words], part p at p mod 3
+    uint32_t *ckey = dyn + 3 * g.bm_words;           // [2][PCAP]
     int32_t *cid = (int32_t *)(ckey + 2 * PCAP);     // [2][PCAP]
     if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];
     if (tid == 0) pl.ncand[0] = pl.ncand[1] = 0;
 
-    // prologue: parts 0 and 1 completed, part 0's row max known, part 2 loading and its
-    // bitmap built.  Data and control waves then run loops of their own (the branch is on
+    // prologue: parts 0 and 1 completed, part 0's row max known (exchanged while part 1
+    // is completed), part 2 loading and its bitmap built.  Data and control waves then run loops of their own (the branch is on
     // the wavefront index, uniform in each wavefront), meeting at one barrier per stage.
     const bool t0 = task_valid(a, 0, g, w), t1 = task_valid(a, 1, g, w),
                t2 = task_valid(a, 2, g, w);
@@ -666,10 +670,10 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         issue_loads(B0, a, r0, t0, g);
         issue_loads(B1, a, r1, t1, g);
         __syncthreads();
-        issue_loads(B2, a, r2, t2, g);
         if (t0) complete_part(B0, g, bm, pl.cfg[0], pl, 0);
-        if (t1) complete_part(B1, g, bm + g.bm_words, pl.cfg[1], pl, 1);
-        __syncthreads();
+        __syncthreads();                         // part 0's max is exchanged meanwhile
+        issue_loads(B2, a, r2, t2, g);
+        if (t1) complete_part(B1, g, bm + g.bm_words, pl.cfg[1], pl, 1);   // slot 1
         // buffer roles rotate with period 3
         for (int s = 0; s < a.stages; s += 3) {
             data_stage(B0, B2, s, a, g, w, bm, ckey, cid, pl);
@@ -698,6 +702,10 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
             bitmap_build(bm + g.bm_words, f1, a, r1, g);
             set_cfg(pl.cfg[1], f1.P, row_pen(f1));
         }
+        if (t2) {
+            bitmap_build(bm + 2 * g.bm_words, f2, a, r2, g);
+            set_cfg(pl.cfg[2], f2.P, row_pen(f2));
+        }
         __syncthreads();
         __syncthreads();
         if (t0) control_publish(a, r0, g, pl, 0, 0);
@@ -705,14 +713,11 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
             const uint32_t th = part_theta(pl.lmax[0], pl.cfg[0]);
             if ((tid & 63) == 0) pl.theta[0] = th;
         }
-        if (t2) {
-            bitmap_build(bm, f2, a, r2, g);
-            set_cfg(pl.cfg[2], f2.P, row_pen(f2));
-        }
         if (t0 && !(pl.cfg[0].flags & CFG_GREEDY)) {
             const uint32_t key = poll_rowmax(a, r0);
             if ((tid & 63) == 0) pl.maxkey[0] = key;
         }
+
         for (int s = 0; s < a.stages; ++s) control_stage(s, rp, a, g, w, bm, ckey, cid, pl);
     }
     __builtin_amdgcn_s_setprio(0);
@@ -746,7 +751,7 @@ int qs_pipe_supported(int n_rows, int n_vocab, int64_t row_stride, const void *l
 
 size_t qs_pipe_lds_bytes(int n_vocab) {
     const int part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
-    const size_t pipe = sizeof(uint32_t) * (2 * ((size_t)part_len / 32 + 1) + 4 * PCAP);
+    const size_t pipe = sizeof(uint32_t) * (3 * ((size_t)part_len / 32 + 1) + 4 * PCAP);
     const size_t epi = sizeof(uint32_t) * 2 * FCAP + sizeof(uint64_t) * SORT_CAP;
     const size_t fl = sizeof(FullLds<NT>);
     size_t m = pipe > epi ? pipe : epi;
