@@ -56,6 +56,10 @@ constexpr int UP = 5;                // float4 per data thread per part
 constexpr int PCAP = 512;            // candidates per part (<= Scratch::ccap)
 constexpr int FCAP = 4096;           // candidates gathered per row in the epilogue
 constexpr int NDW = NWV - 1;         // data waves
+// Thread max keys of data wave j start at j*LM_STRIDE: an odd stride puts the 16 keys
+// that lanes 4j..4j+3 of the control wave read at once (j + 16q + i mod 64) in distinct
+// LDS banks.
+constexpr int LM_STRIDE = 65;
 
 __constant__ uint64_t c_exp_tab_p[QS_EXPF_TAB_N] = QS_EXPF_TABLE_INIT;
 
@@ -96,7 +100,8 @@ struct PipeLds {
     uint32_t maxkey[3];              // row max keys (by part index mod 3)
     uint32_t theta[4];               // candidate threshold keys (by part index mod 4)
     PartCfg cfg[4];                  // by part index mod 4
-    uint32_t lmax[2][DT];            // each data thread's max key of a completed part
+    uint32_t lmax[2][NDW * LM_STRIDE];   // each data thread's max key of a completed part
+                                         // (data wave j at j*LM_STRIDE: see LM_STRIDE)
     RowTotals tot;
     int offs[PARTS + 1];
     float gbv;
@@ -209,7 +214,7 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
             pl.wbi[par][wv] = bi;
         }
     } else {
-        pl.lmax[par][dt] = f2key(mx);
+        pl.lmax[par][(wv - 1) * LM_STRIDE + lane] = f2key(mx);
     }
 }
 
@@ -362,7 +367,7 @@ __device__ __forceinline__ uint32_t part_max(const uint32_t *lm) {
     const int lane = threadIdx.x & 63;
     uint32_t m = 0u;
 #pragma unroll
-    for (int j = 0; j < NDW; ++j) m = max(m, lm[j * 64 + lane]);
+    for (int j = 0; j < NDW; ++j) m = max(m, lm[j * LM_STRIDE + lane]);
     return wave_max_u(m);
 }
 
@@ -389,7 +394,7 @@ __device__ __forceinline__ uint32_t part_theta(const uint32_t *lm, const PartCfg
         const int j = lane >> 2;
         uint32_t t1 = 0u, t2 = 0u, t3 = 0u;          // thread max keys are never 0
         if (j < NDW) {
-            const uint32_t *src = lm + j * 64 + (lane & 3) * 16;
+            const uint32_t *src = lm + j * LM_STRIDE + (lane & 3) * 16;
 #pragma unroll
             for (int i = 0; i < 16; ++i) top3_insert(t1, t2, t3, src[i]);
         }
@@ -413,7 +418,7 @@ __device__ __forceinline__ uint32_t part_theta(const uint32_t *lm, const PartCfg
     } else {
         uint32_t k[NDW];
 #pragma unroll
-        for (int j = 0; j < NDW; ++j) k[j] = lm[j * 64 + lane];
+        for (int j = 0; j < NDW; ++j) k[j] = lm[j * LM_STRIDE + lane];
         th = wave_kth(k, cf.kw, DT);
     }
     return th <= KEY_NEG_INF ? KEY_NEG_INF + 1u : th;   // -inf and NaN never qualify
@@ -499,6 +504,17 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
     }
     __syncthreads();
     const int l0 = row * PARTS;
+    // The first SPEC candidates of every part, loaded with the totals (one round trip;
+    // a part with more is completed below).
+    constexpr int SPEC = NT / PARTS;
+    const int sp = tid / SPEC, si = tid % SPEC;
+    uint32_t skey = 0u;
+    int32_t sid = 0;
+    if (!row_greedy(P)) {
+        const int64_t src = (int64_t)(l0 + sp) * PCAP + si;
+        skey = ld_dev(&sc.ckey[src]);
+        sid = ld_dev(&sc.cid[src]);
+    }
     if (tid < 64) {
         const bool have = lane < PARTS;
         if (row_greedy(P)) {
@@ -546,29 +562,17 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
         RowTotals t = pl.tot;
         t.total = pl.offs[PARTS];
         if (t.total <= FCAP && isfinite(t.maxl * P.inv_t)) {
-            // every load issued before any is stored to LDS
-            uint32_t kk[FCAP / NT];
-            int32_t ii[FCAP / NT];
-#pragma unroll
-            for (int q = 0; q < FCAP / NT; ++q) {
-                const int j = q * NT + tid;
-                kk[q] = 0u;
-                ii[q] = 0;
-                if (j < t.total) {
-                    int p = 0;
-#pragma unroll
-                    for (int o = 1; o < PARTS; ++o) p += j >= pl.offs[o] ? 1 : 0;
-                    const int64_t src = (int64_t)(l0 + p) * PCAP + (j - pl.offs[p]);
-                    kk[q] = ld_dev(&sc.ckey[src]);
-                    ii[q] = ld_dev(&sc.cid[src]);
-                }
+            const int n_sp = pl.offs[sp + 1] - pl.offs[sp];
+            if (si < n_sp) {
+                keys[pl.offs[sp] + si] = skey;
+                ids[pl.offs[sp] + si] = sid;
             }
-#pragma unroll
-            for (int q = 0; q < FCAP / NT; ++q) {
-                const int j = q * NT + tid;
-                if (j < t.total) {
-                    keys[j] = kk[q];
-                    ids[j] = ii[q];
+            for (int p = 0; p < PARTS; ++p) {            // parts with more than SPEC
+                const int n = pl.offs[p + 1] - pl.offs[p];
+                for (int j = SPEC + tid; j < n; j += NT) {
+                    const int64_t src = (int64_t)(l0 + p) * PCAP + j;
+                    keys[pl.offs[p] + j] = ld_dev(&sc.ckey[src]);
+                    ids[pl.offs[p] + j] = ld_dev(&sc.cid[src]);
                 }
             }
         }
@@ -592,11 +596,17 @@ __device__ __forceinline__ void data_stage(float4 (&cur)[UP], float4 (&ld)[UP], 
     const int r3 = task_row(s + 3, w, g.rps);
     const int p0 = s & 1;
     __syncthreads();
+    // The SIMD issues for the wavefront of highest priority first (then the oldest): each
+    // data wavefront lowers its priority as it gets through the stage, so the ones behind
+    // catch up and the SIMD keeps several wavefronts to switch between until the end.
+    __builtin_amdgcn_s_setprio(2);
     if (v0)
         sum_part(cur, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
                  pl.theta[s & 3], pl, p0);
+    __builtin_amdgcn_s_setprio(1);
     issue_loads(cur, a, r3, v3, g);
     if (v2) complete_part(ld, g, bm + ((s + 2) % 3) * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // One stage, control wave: publish part s+1's max (completed during the previous stage),
