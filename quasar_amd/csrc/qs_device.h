@@ -180,6 +180,38 @@ __device__ __forceinline__ uint32_t wave_kth(const uint32_t (&k)[Q], int K, int 
     return th;
 }
 
+// A threshold that keeps at least K and, where ties allow, at most `cap` of the keys a
+// wavefront holds Q per lane (0: no key): the largest prefix th found bit by bit, as in
+// wave_kth, with at least K keys >= th, stopping as soon as at most `cap` keys remain at
+// or above it (all keys when `total` <= cap).  Every key among the K largest (ties kept)
+// is at or above it.
+template <int Q>
+__device__ __forceinline__ uint32_t wave_bracket(const uint32_t (&k)[Q], int K, int cap, int total) {
+    uint32_t kmx = 0u, kmn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        kmx = k[q] > kmx ? k[q] : kmx;
+        kmn = (k[q] != 0u && k[q] < kmn) ? k[q] : kmn;
+    }
+    kmx = wave_max_u(kmx);
+    kmn = wave_min_u(kmn);
+    if (kmx == kmn || total <= cap) return kmn;
+    int b = 31 - __builtin_clz(kmx ^ kmn);
+    uint32_t th = kmx & ~((2u << b) - 1u);        // (2u << 31) wraps to 0: no common bits
+    int cur = total;                              // keys at or above th
+    for (; b >= 0 && cur > cap; --b) {
+        const uint32_t c = th | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) cnt += __popcll(__ballot(k[q] >= c));
+        if (cnt >= K) {
+            th = c;
+            cur = cnt;
+        }
+    }
+    return th;
+}
+
 // The same sort for 32-bit values.
 template <int SIZE, int S>
 __device__ __forceinline__ void bitonic_step_u32(uint32_t &v, int lane) {
@@ -935,10 +967,12 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-// decide_row's decision for one row by one wavefront, in registers: the K-th largest
-// candidate key by a bit-serial ballot select, exact p per lane, a 64-lane bitonic sort by
-// (p desc, id asc), the proof of the prefix and sample.c:153-178 through lane reads.  For
-// rows with at most WAVE_CAND gathered candidates whose top K (ties kept) are at most 64.
+// decide_row's decision for one row by one wavefront, in registers: a threshold keeping
+// the K largest candidate keys and at most 64 (a bit-serial ballot bracket), exact p per
+// lane, a 64-lane bitonic sort by (p desc, id asc), the proof of the prefix and
+// sample.c:153-178 through lane reads.  Keys below the threshold bound the probability of
+// everything not kept, as the parts' rejected keys do.  For rows with at most WAVE_CAND
+// gathered candidates and top-k at most 64 whose top K (ties kept) are at most 64.
 // Returns 0 when the row is decided and recorded, 1 when it needs decide_row (too many
 // candidates, non-finite maximum, overflowed lists), 2 when the proof does not cover the
 // cuts (the caller runs full_row).  scratch: 64 u64 of LDS private to this wavefront.
@@ -963,14 +997,15 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
         k[q] = valid[q] ? keys[j] : 0u;
         idv[q] = valid[q] ? ids[j] : 0;
     }
-    // the K-th largest key (ties kept above it), as block_kth does
+    // a threshold keeping the K largest keys (ties kept) and at most 64 in all
     const int K = row_ksel(P);
+    if (K > 64) return 1;
     uint32_t th = 0u;
-    if (t.total > K) {
+    if (t.total > 64) {
         uint32_t kk[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) kk[q] = valid[q] ? k[q] : 0u;
-        th = wave_kth(kk, K, t.total);
+        th = wave_bracket(kk, K, 64, t.total);
     }
     int n_kept = 0;
     uint32_t myrej = 0u;

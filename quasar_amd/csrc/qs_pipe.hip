@@ -70,6 +70,8 @@ struct PipeArgs {
     int n_rows;
     int part_len;                    // elements per part (multiple of 4)
     int stages;
+    int stages_pad;                  // stages rounded up to a multiple of 3: the stage loops
+                                     // run whole rotations of the three register buffers
     RowState st;
     Scratch sc;
     int32_t *out;
@@ -107,6 +109,10 @@ struct PipeLds {
     float gbv;
     int gbi;
 };
+
+// History bitmap words of a part (one bit per logit, rounded up to whole 16-byte groups so
+// that each of the three slots starts 16-byte aligned and is cleared with 16-byte stores).
+__host__ __device__ constexpr int bitmap_words(int part_len) { return (part_len / 32 + 1 + 3) / 4 * 4; }
 
 struct Geo {                         // this workgroup's part of every row
     int part, c_lo, c_hi, lo, rps, bm_words;
@@ -346,7 +352,8 @@ __device__ __forceinline__ void bitmap_build(uint32_t *bm, const RowFetch &f, co
                                              int row, const Geo &g) {
     const int lane = threadIdx.x & 63;
     if (!row_pen(f)) return;
-    for (int j = lane; j < g.bm_words; j += 64) bm[j] = 0u;
+    uint4 *b4 = (uint4 *)bm;                        // bm_words is a multiple of 4
+    for (int j = lane; j < g.bm_words / 4; j += 64) b4[j] = make_uint4(0u, 0u, 0u, 0u);
     const int hi = g.c_hi * 4, cap = f.P.ring_cap;
     auto mark = [&](int p, int id) {
         int d = p - f.head;
@@ -382,37 +389,47 @@ __device__ __forceinline__ void top3_insert(uint32_t &t1, uint32_t &t2, uint32_t
     t3 = n3;
 }
 
+// Control wave: the three largest thread max keys of each data wave, lanes 4j..4j+3 holding
+// data wave j's (each scans 16 of its 64 keys, then the quad merges); zeros past the data
+// waves.  Their lane maximum is the part's max key.
+struct Top3 {
+    uint32_t t1, t2, t3;
+};
+__device__ __forceinline__ Top3 quad_top3(const uint32_t *lm) {
+    const int lane = threadIdx.x & 63, j = lane >> 2;
+    uint32_t t1 = 0u, t2 = 0u, t3 = 0u;              // thread max keys are never 0
+    if (j < NDW) {
+        const uint32_t *src = lm + j * LM_STRIDE + (lane & 3) * 16;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) top3_insert(t1, t2, t3, src[i]);
+    }
+    {
+        const uint32_t o1 = xor_lane<1>(t1), o2 = xor_lane<1>(t2), o3 = xor_lane<1>(t3);
+        top3_insert(t1, t2, t3, o1);
+        top3_insert(t1, t2, t3, o2);
+        top3_insert(t1, t2, t3, o3);
+    }
+    {
+        const uint32_t o1 = xor_lane<2>(t1), o2 = xor_lane<2>(t2), o3 = xor_lane<2>(t3);
+        top3_insert(t1, t2, t3, o1);
+        top3_insert(t1, t2, t3, o2);
+        top3_insert(t1, t2, t3, o3);
+    }
+    return Top3{t1, t2, t3};
+}
+
 // Control wave: the part's candidate threshold, the kw-th largest of a set of thread max
 // keys (kw distinct logits of the part reach it; the part keeps every logit at or above
 // it, and every other one lies below it).  The set is each data wave's three largest
-// (lanes 4j..4j+3 keep the top three of data wave j's 64 keys, 16 each, then merge within
-// the quad), or, when kw exceeds those, all of them.
-__device__ __forceinline__ uint32_t part_theta(const uint32_t *lm, const PartCfg &cf) {
+// (from quad_top3) or, when kw exceeds those, all of them.
+__device__ __forceinline__ uint32_t part_theta(const Top3 &tp, const uint32_t *lm,
+                                               const PartCfg &cf) {
     const int lane = threadIdx.x & 63;
     uint32_t th;
     if (cf.kw <= 3 * NDW) {
-        const int j = lane >> 2;
-        uint32_t t1 = 0u, t2 = 0u, t3 = 0u;          // thread max keys are never 0
-        if (j < NDW) {
-            const uint32_t *src = lm + j * LM_STRIDE + (lane & 3) * 16;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) top3_insert(t1, t2, t3, src[i]);
-        }
-        {
-            const uint32_t o1 = xor_lane<1>(t1), o2 = xor_lane<1>(t2), o3 = xor_lane<1>(t3);
-            top3_insert(t1, t2, t3, o1);
-            top3_insert(t1, t2, t3, o2);
-            top3_insert(t1, t2, t3, o3);
-        }
-        {
-            const uint32_t o1 = xor_lane<2>(t1), o2 = xor_lane<2>(t2), o3 = xor_lane<2>(t3);
-            top3_insert(t1, t2, t3, o1);
-            top3_insert(t1, t2, t3, o2);
-            top3_insert(t1, t2, t3, o3);
-        }
         // the 45 values one per lane (lane 4j+q: wave j's (q+1)-th), sorted: the kw-th
         const int q = lane & 3;
-        uint32_t v = (j < NDW && q < 3) ? (q == 0 ? t1 : q == 1 ? t2 : t3) : 0u;
+        uint32_t v = ((lane >> 2) < NDW && q < 3) ? (q == 0 ? tp.t1 : q == 1 ? tp.t2 : tp.t3) : 0u;
         v = wave_sort_desc_u32(v);
         th = (uint32_t)__builtin_amdgcn_readlane((int)v, cf.kw - 1);
     } else {
@@ -424,25 +441,35 @@ __device__ __forceinline__ uint32_t part_theta(const uint32_t *lm, const PartCfg
     return th <= KEY_NEG_INF ? KEY_NEG_INF + 1u : th;   // -inf and NaN never qualify
 }
 
-// Control wave: publish the completed part's max (sampling) or best (greedy).
-__device__ __forceinline__ void control_publish(const PipeArgs &a, int row, const Geo &g,
+// Control wave: publish the completed part's max (sampling; returns the per-wave top three
+// for the part's threshold) or best (greedy).
+__device__ __forceinline__ Top3 control_publish(const PipeArgs &a, int row, const Geo &g,
                                                 PipeLds &pl, int par, int cfg_slot) {
     const int lane = threadIdx.x & 63;
-    const bool greedy = (pl.cfg[cfg_slot].flags & CFG_GREEDY) != 0;
-    const uint32_t mk = greedy ? 0u : part_max(pl.lmax[par]);
-    if (lane != 0) return;
+    const PartCfg &cf = pl.cfg[cfg_slot];
     const int li = row * PARTS + g.part;
-    if (greedy) {
-        float v0 = pl.wbv[par][1];
-        int i0 = pl.wbi[par][1];
-        for (int k = 2; k < NWV; ++k) best_combine(v0, i0, pl.wbv[par][k], pl.wbi[par][k]);
-        st_dev(&a.sc.bestv[li], v0);
-        st_dev(&a.sc.besti[li], i0);
-        stores_done();
-        add_dev(&a.sc.done[row], 1);
-        return;
+    Top3 tp{0u, 0u, 0u};
+    if (cf.flags & CFG_GREEDY) {
+        if (lane == 0) {
+            float v0 = pl.wbv[par][1];
+            int i0 = pl.wbi[par][1];
+            for (int k = 2; k < NWV; ++k) best_combine(v0, i0, pl.wbv[par][k], pl.wbi[par][k]);
+            st_dev(&a.sc.bestv[li], v0);
+            st_dev(&a.sc.besti[li], i0);
+            stores_done();
+            add_dev(&a.sc.done[row], 1);
+        }
+        return tp;
     }
-    st_dev(&a.sc.rowmax[li], mk);                 // seen by the partners' polls
+    uint32_t mk;
+    if (cf.kw <= 3 * NDW) {
+        tp = quad_top3(pl.lmax[par]);
+        mk = wave_max_u(tp.t1);
+    } else {
+        mk = part_max(pl.lmax[par]);
+    }
+    if (lane == 0) st_dev(&a.sc.rowmax[li], mk);  // seen by the partners' polls
+    return tp;
 }
 
 // Control wave: store a summed part's results; control_release announces them once every
@@ -464,14 +491,12 @@ __device__ __forceinline__ bool control_store(const PipeArgs &a, int row, const 
         st_dev(&gk[j], ckey[j]);
         st_dev(&gi[j], cid[j]);
     }
+    // the data waves' partial sums and window counts, one per lane (every data wave wrote
+    // its own when the part is live)
+    const bool mine = live && lane < NDW;
+    const double t = wave_sum_d(mine ? pl.wsum[par][lane + 1] : 0.0);
+    const int ct = wave_sum_i(mine ? pl.wcnt[par][lane + 1] : 0);
     if (lane == 0) {
-        double t = 0.0;
-        int ct = 0;
-        if (live)
-            for (int k = 1; k < NWV; ++k) {
-                t += pl.wsum[par][k];
-                ct += pl.wcnt[par][k];
-            }
         st_dev(&a.sc.psum[li], t);
         st_dev(&a.sc.pcnt[li], ct);
         st_dev(&a.sc.ccnt[li], n);
@@ -626,7 +651,8 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
     __syncthreads();
     const RowFetch f3 = rp;                      // part s+3's row, fetched last stage
     if (task_valid(a, s + 4, g, w)) rp = fetch_row(a, task_row(s + 4, w, g.rps));
-    if (v1) control_publish(a, r1, g, pl, p1, (s + 1) & 3);
+    Top3 tp{0u, 0u, 0u};
+    if (v1) tp = control_publish(a, r1, g, pl, p1, (s + 1) & 3);
     const bool sv = s >= 1 && task_valid(a, s - 1, g, w);
     const int rs = task_row(s - 1, w, g.rps);
     bool rel = false;
@@ -634,7 +660,7 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
         rel = control_store(a, rs, g, pl.maxkey[(s + 2) % 3], pl.theta[(s + 3) & 3],
                             ckey + p1 * PCAP, cid + p1 * PCAP, pl.cfg[(s + 3) & 3], pl, p1);
     if (v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY)) {
-        const uint32_t th = part_theta(pl.lmax[p1], pl.cfg[(s + 1) & 3]);
+        const uint32_t th = part_theta(tp, pl.lmax[p1], pl.cfg[(s + 1) & 3]);
         if (lane == 0) pl.theta[(s + 1) & 3] = th;
     }
     if (v3) {
@@ -649,7 +675,7 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
 }
 
 __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
-    extern __shared__ uint32_t dyn[];
+    extern __shared__ __align__(16) uint32_t dyn[];
     __shared__ PipeLds pl;
     const int w = blockIdx.x, tid = threadIdx.x;
     const bool data = tid >= 64;
@@ -660,7 +686,7 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     const int p_hi = min(g.lo + a.part_len, a.vocab);
     g.c_lo = g.lo >> 2;
     g.c_hi = p_hi >> 2;
-    g.bm_words = a.part_len / 32 + 1;
+    g.bm_words = bitmap_words(a.part_len);
     uint32_t *bm = dyn;                              // [3][bm_words], part p at p mod 3
     uint32_t *ckey = dyn + 3 * g.bm_words;           // [2][PCAP]
     int32_t *cid = (int32_t *)(ckey + 2 * PCAP);     // [2][PCAP]
@@ -678,18 +704,19 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         float4 B0[UP], B1[UP], B2[UP];
         __syncthreads();                         // the control wave's fetches go first
         issue_loads(B0, a, r0, t0, g);
+        __syncthreads();                         // every wave's part 0 ahead of part 1
         issue_loads(B1, a, r1, t1, g);
         __syncthreads();
         if (t0) complete_part(B0, g, bm, pl.cfg[0], pl, 0);
         __syncthreads();                         // part 0's max is exchanged meanwhile
         issue_loads(B2, a, r2, t2, g);
         if (t1) complete_part(B1, g, bm + g.bm_words, pl.cfg[1], pl, 1);   // slot 1
-        // buffer roles rotate with period 3
-        for (int s = 0; s < a.stages; s += 3) {
+        // buffer roles rotate with period 3; whole rotations only (stages past the last
+        // one do nothing), so every pass through the loop leaves the same loads in flight
+        // (the next part's, in B2) and each wait covers only the loads it needs
+        for (int s = 0; s < a.stages_pad; s += 3) {
             data_stage(B0, B2, s, a, g, w, bm, ckey, cid, pl);
-            if (s + 1 >= a.stages) break;
             data_stage(B1, B0, s + 1, a, g, w, bm, ckey, cid, pl);
-            if (s + 2 >= a.stages) break;
             data_stage(B2, B1, s + 2, a, g, w, bm, ckey, cid, pl);
         }
     } else {
@@ -704,6 +731,7 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         if (t2) f2 = fetch_row(a, r2);
         if (t3) rp = fetch_row(a, task_row(3, w, g.rps));
         __syncthreads();
+        __syncthreads();
         if (t0) {
             bitmap_build(bm, f0, a, r0, g);
             set_cfg(pl.cfg[0], f0.P, row_pen(f0));
@@ -712,15 +740,16 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
             bitmap_build(bm + g.bm_words, f1, a, r1, g);
             set_cfg(pl.cfg[1], f1.P, row_pen(f1));
         }
-        if (t2) {
+        __syncthreads();
+        if (t2) {                                    // used from stage 0 on
             bitmap_build(bm + 2 * g.bm_words, f2, a, r2, g);
             set_cfg(pl.cfg[2], f2.P, row_pen(f2));
         }
         __syncthreads();
-        __syncthreads();
-        if (t0) control_publish(a, r0, g, pl, 0, 0);
+        Top3 tp0{0u, 0u, 0u};
+        if (t0) tp0 = control_publish(a, r0, g, pl, 0, 0);
         if (t0 && !(pl.cfg[0].flags & CFG_GREEDY)) {
-            const uint32_t th = part_theta(pl.lmax[0], pl.cfg[0]);
+            const uint32_t th = part_theta(tp0, pl.lmax[0], pl.cfg[0]);
             if ((tid & 63) == 0) pl.theta[0] = th;
         }
         if (t0 && !(pl.cfg[0].flags & CFG_GREEDY)) {
@@ -728,12 +757,12 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
             if ((tid & 63) == 0) pl.maxkey[0] = key;
         }
 
-        for (int s = 0; s < a.stages; ++s) control_stage(s, rp, a, g, w, bm, ckey, cid, pl);
+        for (int s = 0; s < a.stages_pad; ++s) control_stage(s, rp, a, g, w, bm, ckey, cid, pl);
     }
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
-    {                                                // the last summed part
-        const int s = a.stages - 1;
+    {                                // the last summed part, unless the loop stored it
+        const int s = a.stages_pad - 1;
         if (!data && s >= 0 && task_valid(a, s, g, w))
             if (control_store(a, task_row(s, w, g.rps), g, pl.maxkey[s % 3], pl.theta[s & 3],
                               ckey + (s & 1) * PCAP, cid + (s & 1) * PCAP, pl.cfg[s & 3], pl,
@@ -761,7 +790,7 @@ int qs_pipe_supported(int n_rows, int n_vocab, int64_t row_stride, const void *l
 
 size_t qs_pipe_lds_bytes(int n_vocab) {
     const int part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
-    const size_t pipe = sizeof(uint32_t) * (3 * ((size_t)part_len / 32 + 1) + 4 * PCAP);
+    const size_t pipe = sizeof(uint32_t) * (3 * (size_t)bitmap_words(part_len) + 4 * PCAP);
     const size_t epi = sizeof(uint32_t) * 2 * FCAP + sizeof(uint64_t) * SORT_CAP;
     const size_t fl = sizeof(FullLds<NT>);
     size_t m = pipe > epi ? pipe : epi;
@@ -796,6 +825,7 @@ int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vo
     a.part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
     const int rps = grid / PARTS;
     a.stages = (n_rows + rps - 1) / rps;
+    a.stages_pad = (a.stages + 2) / 3 * 3;
     a.st = st;
     a.sc = sc;
     a.out = out;
