@@ -325,26 +325,52 @@ __device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row) {
 // stage before the row's part is completed, so the loads complete during other work.
 constexpr int RING_PF = 8;
 struct RowFetch {
-    qs_row_param P;
-    int len, head;
+    int pw;                          // lane i < 8: word i of the row's qs_row_param
+    int lw, hw;                      // history length and ring head (every lane)
     int slot[RING_PF];
+    __device__ qs_row_param param() const {   // read out of the lanes when used
+        qs_row_param P;
+        P.temperature = __int_as_float(__builtin_amdgcn_readlane(pw, 0));
+        P.top_p = __int_as_float(__builtin_amdgcn_readlane(pw, 1));
+        P.min_p = __int_as_float(__builtin_amdgcn_readlane(pw, 2));
+        P.repeat_penalty = __int_as_float(__builtin_amdgcn_readlane(pw, 3));
+        P.top_k = __builtin_amdgcn_readlane(pw, 4);
+        P.ring_cap = __builtin_amdgcn_readlane(pw, 5);
+        P.inv_t = __int_as_float(__builtin_amdgcn_readlane(pw, 6));
+        P.pad = 0;
+        return P;
+    }
+    __device__ int len() const { return __builtin_amdgcn_readfirstlane(lw); }
+    __device__ int head() const { return __builtin_amdgcn_readfirstlane(hw); }
 };
+// Buffer loads at offsets the compiler treats as per-lane, so it moves nothing out of
+// them into scalar registers (which would wait for them) before they are used.
+__device__ __forceinline__ int lane_load(const void *base, int bytes, int off) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, BUF_WORD3);
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+}
 __device__ __forceinline__ RowFetch fetch_row(const PipeArgs &a, int row) {
     const int lane = threadIdx.x & 63;
+    int vz;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vz));     // zero, as a per-lane value
     RowFetch f;
-    f.P = a.st.prm[row];
-    f.len = a.st.hlen[row];
-    f.head = a.st.hhead[row];
+    static_assert(sizeof(qs_row_param) == 32, "eight words of parameters");
+    const int nb = a.n_rows * 4;
+    f.pw = lane_load(a.st.prm, a.n_rows * 32, row * 32 + (lane & 7) * 4);
+    f.lw = lane_load(a.st.hlen, nb, row * 4 + vz);
+    f.hw = lane_load(a.st.hhead, nb, row * 4 + vz);
+    // the ring slots: slots past the row's ring read as 0 without a memory access (and are
+    // never marked, p >= ring_stride >= cap)
     const int32_t *ring = a.st.ring + (int64_t)row * a.st.ring_stride;
 #pragma unroll
-    for (int q = 0; q < RING_PF; ++q) {
-        const int p = q * 64 + lane;
-        f.slot[q] = p < a.st.ring_stride ? ring[p] : -1;
-    }
+    for (int q = 0; q < RING_PF; ++q)
+        f.slot[q] = lane_load(ring, a.st.ring_stride * 4, (q * 64 + lane) * 4);
     return f;
 }
 __device__ __forceinline__ bool row_pen(const RowFetch &f) {
-    return f.P.repeat_penalty > 1.0f && f.len > 0 && f.P.ring_cap > 0;
+    const qs_row_param P = f.param();
+    return P.repeat_penalty > 1.0f && f.len() > 0 && P.ring_cap > 0;
 }
 
 // Control wave: the history bitmap of this workgroup's part of a row.
@@ -354,11 +380,11 @@ __device__ __forceinline__ void bitmap_build(uint32_t *bm, const RowFetch &f, co
     if (!row_pen(f)) return;
     uint4 *b4 = (uint4 *)bm;                        // bm_words is a multiple of 4
     for (int j = lane; j < g.bm_words / 4; j += 64) b4[j] = make_uint4(0u, 0u, 0u, 0u);
-    const int hi = g.c_hi * 4, cap = f.P.ring_cap;
+    const int hi = g.c_hi * 4, cap = f.param().ring_cap, head = f.head(), len = f.len();
     auto mark = [&](int p, int id) {
-        int d = p - f.head;
+        int d = p - head;
         if (d < 0) d += cap;
-        if (p < cap && d < f.len && id >= g.lo && id < hi)
+        if (p < cap && d < len && id >= g.lo && id < hi)
             atomicOr(&bm[(id - g.lo) >> 5], 1u << ((id - g.lo) & 31));
     };
 #pragma unroll
@@ -665,7 +691,7 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
     }
     if (v3) {
         bitmap_build(bm + (s % 3) * g.bm_words, f3, a, r3, g);   // part s+3's slot
-        set_cfg(pl.cfg[(s + 3) & 3], f3.P, row_pen(f3));   // part s-1's settings are used
+        set_cfg(pl.cfg[(s + 3) & 3], f3.param(), row_pen(f3));   // part s-1's settings are used
     }
     if (rel) control_release(a, rs);
     if (v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY)) {
@@ -690,7 +716,6 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     uint32_t *bm = dyn;                              // [3][bm_words], part p at p mod 3
     uint32_t *ckey = dyn + 3 * g.bm_words;           // [2][PCAP]
     int32_t *cid = (int32_t *)(ckey + 2 * PCAP);     // [2][PCAP]
-    if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];
     if (tid == 0) pl.ncand[0] = pl.ncand[1] = 0;
 
     // prologue: parts 0 and 1 completed, part 0's row max known (exchanged while part 1
@@ -730,20 +755,21 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         if (t1) f1 = fetch_row(a, r1);
         if (t2) f2 = fetch_row(a, r2);
         if (t3) rp = fetch_row(a, task_row(3, w, g.rps));
+        if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];   // after the fetches
         __syncthreads();
         __syncthreads();
         if (t0) {
             bitmap_build(bm, f0, a, r0, g);
-            set_cfg(pl.cfg[0], f0.P, row_pen(f0));
+            set_cfg(pl.cfg[0], f0.param(), row_pen(f0));
         }
         if (t1) {
             bitmap_build(bm + g.bm_words, f1, a, r1, g);
-            set_cfg(pl.cfg[1], f1.P, row_pen(f1));
+            set_cfg(pl.cfg[1], f1.param(), row_pen(f1));
         }
         __syncthreads();
         if (t2) {                                    // used from stage 0 on
             bitmap_build(bm + 2 * g.bm_words, f2, a, r2, g);
-            set_cfg(pl.cfg[2], f2.P, row_pen(f2));
+            set_cfg(pl.cfg[2], f2.param(), row_pen(f2));
         }
         __syncthreads();
         Top3 tp0{0u, 0u, 0u};
