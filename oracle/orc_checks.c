@@ -44,7 +44,11 @@ void orc_libm_expf_array(const float *x, float *y, long n) {
 
 typedef struct { uint32_t lo, hi; int neg; long bad; } orc_xjob;
 
-/* Walk float bit patterns [lo, hi] of one sign. */
+/* The window variant's extended table (qs_expf_window), built before any walk starts. */
+static uint64_t orc_xtab[QS_EXPF_XTAB_N];
+
+/* Walk float bit patterns [lo, hi] of one sign: qs_expf everywhere and, inside the
+ * window variant's range [-33, 0], qs_expf_window too, against the C library's expf. */
 static long orc_xwalk(const orc_xjob *j) {
     long bad = 0;
     for (uint64_t b = j->lo; b <= j->hi; b++) {
@@ -52,6 +56,7 @@ static long orc_xwalk(const orc_xjob *j) {
         float x = qs_u2f(bits);
         float a = expf(x), c = qs_expf(x);
         if (qs_f2u(a) != qs_f2u(c) && !(isnan(a) && isnan(c))) bad++;
+        if (x <= 0.0f && x >= -33.0f && qs_f2u(qs_expf_window(x, orc_xtab)) != qs_f2u(a)) bad++;
     }
     return bad;
 }
@@ -65,6 +70,7 @@ __attribute__((target("fma"))) static long orc_xwalk_fma(const orc_xjob *j) {
         float x = qs_u2f(bits);
         float a = expf(x), c = qs_expf(x);
         if (qs_f2u(a) != qs_f2u(c) && !(isnan(a) && isnan(c))) bad++;
+        if (x <= 0.0f && x >= -33.0f && qs_f2u(qs_expf_window(x, orc_xtab)) != qs_f2u(a)) bad++;
     }
     return bad;
 }
@@ -95,6 +101,7 @@ long orc_check_expf_range(float lo, float hi, int n_threads) {
         np++;
     }
     if (n_threads < 1) n_threads = 1;
+    for (int i = 0; i < QS_EXPF_XTAB_N; i++) orc_xtab[i] = qs_expf_xtab_entry(qs_expf_table_host, i);
     long bad = 0;
     for (int k = 0; k < np; k++) {
         orc_xjob *jobs = (orc_xjob *)calloc((size_t)n_threads, sizeof(orc_xjob));

@@ -490,12 +490,28 @@ __global__ void __launch_bounds__(WG) k_copy(const float4 *x, float4 *y, int64_t
         y[i] = x[i];
 }
 
+// The kernels' expf, element by element.  Inside [-33, 0] the pipelined kernel's 4-wide
+// window variant (qs_expf4_window, extended table) runs too, and a result different from
+// qs_expf_tab's is reported as NaN, so the comparison with the host C library covers both.
 __global__ void __launch_bounds__(WG) k_expf(const float *x, float *y, int64_t n) {
     __shared__ uint64_t tab[QS_EXPF_TAB_N];
+    __shared__ uint64_t xtab[QS_EXPF_XTAB_N];
     if (threadIdx.x < QS_EXPF_TAB_N) tab[threadIdx.x] = c_exp_tab[threadIdx.x];
     __syncthreads();
+    for (int j = threadIdx.x; j < QS_EXPF_XTAB_N; j += WG) xtab[j] = qs_expf_xtab_entry(tab, j);
+    __syncthreads();
     const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
-    if (i < n) y[i] = qs_expf_tab(x[i], tab);
+    if (i < n) {
+        const float v = x[i];
+        float r = qs_expf_tab(v, tab);
+        if (v <= 0.0f && v >= -33.0f) {
+            const float a[4] = {v, v, v, v};
+            float e[4];
+            qs_expf4_window(a, e, xtab);
+            if (__float_as_uint(e[0]) != __float_as_uint(r)) r = __builtin_nanf("");
+        }
+        y[i] = r;
+    }
 }
 
 // ---- host side ----------------------------------------------------------------------------

@@ -92,6 +92,7 @@ constexpr int CFG_GREEDY = 1, CFG_PEN = 2;
 // Shared state of one workgroup besides the dynamic region.
 struct PipeLds {
     DecideLds<NT> dl;
+    uint64_t xtab[QS_EXPF_XTAB_N];   // qs_expf_window's extended table (the sums)
     // hand-offs between the data waves and the control wave, double-buffered by part
     // parity: written for one part while the other part's copy is read
     float wbv[2][NWV];               // greedy: per-wave best value / index
@@ -173,20 +174,31 @@ __device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a
 
 // Data waves: penalty (sample.c:118-128) and each thread's max key (the control wave takes
 // the part's max and candidate threshold from them); greedy rows: the wave's first argmax.
-__device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
+// `mn` receives the least of the thread's logits in float4s 0..UP-2, NaN if one is NaN.
+// The max and min propagate NaN (one v_maximum3 / v_minimum3 per pair of logits, where
+// fmaxf would first quiet each operand); a thread whose max comes out NaN takes the max of
+// its other logits, as sample.c:125-127 does (NaN never wins).  Positions past the part
+// read as -inf: never a max, a candidate or in the window.
+__device__ __forceinline__ float max3n(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+__device__ __forceinline__ float min3n(float a, float b, float c) {
+    return __builtin_elementwise_minimum(__builtin_elementwise_minimum(a, b), c);
+}
+__device__ __forceinline__ void complete_part(float4 (&buf)[UP], float &mn, const Geo &g,
                                               const uint32_t *bm, const PartCfg &cf,
                                               PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float rp = cf.rp;
     const bool pen = (cf.flags & CFG_PEN) != 0;
     const bool greedy = (cf.flags & CFG_GREEDY) != 0;
-    const float qnan = __builtin_nanf("");
     const int dt = data_tid();
     // history bits of float4 u: word (u*DT + dt)/8 = u*DT/8 + dt/8, bits 4*(dt%8).. (DT is a
     // multiple of 8, so the shift is the same for every u)
     const uint32_t *bw = bm + (dt >> 3);
     const uint32_t bsh = (uint32_t)(dt & 7) * 4u;
     float mx = -INFINITY, bv = -INFINITY;
+    mn = INFINITY;
     int bi = -1;
     uint32_t hw[UP];                                 // every history word read at once
 #pragma unroll
@@ -196,7 +208,7 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
         const int c = g.c_lo + u * DT + dt;
         float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
         if (u == UP - 1 && c >= g.c_hi)             // past the part: only the last group
-            w[0] = w[1] = w[2] = w[3] = qnan;
+            w[0] = w[1] = w[2] = w[3] = -INFINITY;
         if (pen) {
             const uint32_t nib = __builtin_amdgcn_ubfe(hw[u], bsh, 4);
             if (__ballot(nib != 0u)) {
@@ -205,13 +217,20 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
                     if ((nib >> k) & 1u) w[k] = penalise(w[k], rp);
             }
         }
-        mx = fmaxf(mx, fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3])));   // NaN never wins
+        mx = max3n(max3n(mx, w[0], w[1]), w[2], w[3]);
+        if (u < UP - 1) mn = min3n(min3n(mn, w[0], w[1]), w[2], w[3]);
         if (greedy) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
                 if (w[k] > bv) { bv = w[k]; bi = 4 * c + k; }
         }
         buf[u] = make_float4(w[0], w[1], w[2], w[3]);
+    }
+    if (mx != mx) {                                  // a NaN among them: the others' max
+        mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < UP; ++u)
+            mx = fmaxf(mx, fmaxf(fmaxf(buf[u].x, buf[u].y), fmaxf(buf[u].z, buf[u].w)));
     }
     if (greedy) {
         wave_best(bv, bi);
@@ -225,12 +244,14 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], const Geo &g,
 }
 
 // Data waves: exact softmax numerators, partial sums, window count and candidates of one
-// part, from registers (sample.c:136-149 per element).  Out-of-window lanes evaluate the
-// exp core at X_OUT, which is exactly +0; a part whose float4 holds no logit at or above
-// the threshold skips the candidate test.
-constexpr float X_OUT = -150.0f;
+// part, from registers (sample.c:136-149 per element).  When the thread minima (`mn`, from
+// complete_part) of the whole wavefront are in the window, float4s 0..UP-2 skip the
+// per-logit window tests; otherwise out-of-window lanes evaluate the exp at X_OUT (inside
+// qs_expf_window's range) and their result is discarded.  A float4 holding no logit at or
+// above the threshold skips the candidate test.
+constexpr float X_OUT = -32.0f;
 
-__device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
+__device__ __forceinline__ void sum_part(const float4 (&buf)[UP], float mn, const Geo &g,
                                          const PartCfg &cf, uint32_t *ckey, int32_t *cid,
                                          uint32_t maxkey, uint32_t th, PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -241,7 +262,8 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
     // candidates: every w >= key2f(th), tested as w*inv_t >= key2f(th)*inv_t (monotone in
     // w, so a superset; rejected logits stay below th)
     const float ths = key2f(th) * inv_t;
-    const uint64_t *tab = pl.dl.tab;
+    const uint64_t *xtab = pl.xtab;
+    const bool wave_in = __ballot(!(mn * inv_t >= thr)) == 0ull;   // NaN is not in
     float xo = X_OUT;
     asm volatile("" : "+v"(xo));                    // a register, selected before the exp
     double acc0 = 0.0, acc1 = 0.0;
@@ -252,28 +274,42 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], const Geo &g,
         const int c = g.c_lo + u * DT + dt;
         const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
         float sc[4];
-        uint64_t in[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            sc[k] = w[k] * inv_t;
-            in[k] = __ballot(sc[k] >= thr);         // NaN (masked or past the part) is out
-            cnt += __popcll(in[k]);
+        for (int k = 0; k < 4; ++k) sc[k] = w[k] * inv_t;
+        uint64_t in[4];
+        bool all;
+        if (u < UP - 1 && wave_in) {                // every lane's four in the window
+            in[0] = in[1] = in[2] = in[3] = ~0ull;
+            cnt += 4 * 64;
+            all = true;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                in[k] = __ballot(sc[k] >= thr);     // NaN (or past the part) is out
+                cnt += __popcll(in[k]);
+            }
+            all = (in[0] & in[1] & in[2] & in[3]) == __ballot(true);
         }
-        const uint64_t all = __ballot(true);
-        if ((in[0] & in[1] & in[2] & in[3]) == all) {   // every lane's four in the window
+        if (all) {
             float xa[4], e[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) xa[k] = sc[k] - msc;
-            qs_expf4_core(xa, e, tab);
+            qs_expf4_window(xa, e, xtab);
             acc0 += (double)e[0];
             acc1 += (double)e[1];
             acc0 += (double)e[2];
             acc1 += (double)e[3];
         } else if (in[0] | in[1] | in[2] | in[3]) {
             float xa[4], e[4];
+            bool ok[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) xa[k] = sc[k] >= thr ? sc[k] - msc : xo;
-            qs_expf4_core(xa, e, tab);
+            for (int k = 0; k < 4; ++k) {
+                ok[k] = sc[k] >= thr;
+                xa[k] = ok[k] ? sc[k] - msc : xo;
+            }
+            qs_expf4_window(xa, e, xtab);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) e[k] = ok[k] ? e[k] : 0.0f;
             acc0 += (double)e[0];
             acc1 += (double)e[1];
             acc0 += (double)e[2];
@@ -638,7 +674,8 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
 
 // One stage, data waves: sum part s (in `cur`), issue the loads of part s+3 into `cur`,
 // complete part s+2 (in `ld`, loaded during the previous stage).
-__device__ __forceinline__ void data_stage(float4 (&cur)[UP], float4 (&ld)[UP], int s,
+__device__ __forceinline__ void data_stage(float4 (&cur)[UP], float mcur, float4 (&ld)[UP],
+                                           float &mld, int s,
                                            const PipeArgs &a, const Geo &g, int w,
                                            const uint32_t *bm, uint32_t *ckey, int32_t *cid,
                                            PipeLds &pl) {
@@ -652,11 +689,11 @@ __device__ __forceinline__ void data_stage(float4 (&cur)[UP], float4 (&ld)[UP], 
     // catch up and the SIMD keeps several wavefronts to switch between until the end.
     __builtin_amdgcn_s_setprio(2);
     if (v0)
-        sum_part(cur, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
+        sum_part(cur, mcur, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
                  pl.theta[s & 3], pl, p0);
     __builtin_amdgcn_s_setprio(1);
     issue_loads(cur, a, r3, v3, g);
-    if (v2) complete_part(ld, g, bm + ((s + 2) % 3) * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
+    if (v2) complete_part(ld, mld, g, bm + ((s + 2) % 3) * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
     __builtin_amdgcn_s_setprio(0);
 }
 
@@ -727,22 +764,24 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (wave != 0) {
         float4 B0[UP], B1[UP], B2[UP];
+        float M0 = 0.0f, M1 = 0.0f, M2 = 0.0f;  // thread minima of the parts in B0..B2
         __syncthreads();                         // the control wave's fetches go first
         issue_loads(B0, a, r0, t0, g);
+        for (int j = tid - 64; j < QS_EXPF_XTAB_N; j += DT) pl.xtab[j] = qs_expf_xtab_entry(pl.dl.tab, j);
         __syncthreads();                         // every wave's part 0 ahead of part 1
         issue_loads(B1, a, r1, t1, g);
         __syncthreads();
-        if (t0) complete_part(B0, g, bm, pl.cfg[0], pl, 0);
+        if (t0) complete_part(B0, M0, g, bm, pl.cfg[0], pl, 0);
         __syncthreads();                         // part 0's max is exchanged meanwhile
         issue_loads(B2, a, r2, t2, g);
-        if (t1) complete_part(B1, g, bm + g.bm_words, pl.cfg[1], pl, 1);   // slot 1
+        if (t1) complete_part(B1, M1, g, bm + g.bm_words, pl.cfg[1], pl, 1);   // slot 1
         // buffer roles rotate with period 3; whole rotations only (stages past the last
         // one do nothing), so every pass through the loop leaves the same loads in flight
         // (the next part's, in B2) and each wait covers only the loads it needs
         for (int s = 0; s < a.stages_pad; s += 3) {
-            data_stage(B0, B2, s, a, g, w, bm, ckey, cid, pl);
-            data_stage(B1, B0, s + 1, a, g, w, bm, ckey, cid, pl);
-            data_stage(B2, B1, s + 2, a, g, w, bm, ckey, cid, pl);
+            data_stage(B0, M0, B2, M2, s, a, g, w, bm, ckey, cid, pl);
+            data_stage(B1, M1, B0, M0, s + 1, a, g, w, bm, ckey, cid, pl);
+            data_stage(B2, M2, B1, M1, s + 2, a, g, w, bm, ckey, cid, pl);
         }
     } else {
         // the control wave's steps are on every stage's critical path: it issues ahead of
