@@ -236,15 +236,50 @@ __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
     return v;
 }
 
-// Inclusive prefix sum over the lanes.
-__device__ __forceinline__ double wave_scan_d(double v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double t = __shfl_up(v, o, 64);
-        if (lane >= o) v += t;
+// x from the lane a DPP control names, 0 where there is none (rows outside ROWS, lanes
+// shifted in from outside the row).
+template <int CTRL, int ROWS, typename T>
+__device__ __forceinline__ T dpp_shift(T x) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+    if constexpr (sizeof(T) == 4) {
+        const int b = __builtin_bit_cast(int, x);
+        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, b, CTRL, ROWS, 0xF, false));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, x);
+        const uint32_t rlo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROWS, 0xF, false);
+        const uint32_t rhi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROWS, 0xF, false);
+        return __builtin_bit_cast(T, ((uint64_t)rhi << 32) | rlo);
     }
+}
+// Inclusive prefix sum over the lanes in DPP moves: shifts by 1, 2, 4 and 8 within each
+// row of 16, then rows 1 and 3 add lane 15 of the row below, rows 2 and 3 lane 31.
+template <typename T>
+__device__ __forceinline__ T wave_scan(T v) {
+    v += dpp_shift<0x111, 0xF>(v);          // row_shr:1
+    v += dpp_shift<0x112, 0xF>(v);          // row_shr:2
+    v += dpp_shift<0x114, 0xF>(v);          // row_shr:4
+    v += dpp_shift<0x118, 0xF>(v);          // row_shr:8
+    v += dpp_shift<0x142, 0xA>(v);          // row_bcast:15 into rows 1 and 3
+    v += dpp_shift<0x143, 0xC>(v);          // row_bcast:31 into rows 2 and 3
     return v;
+}
+__device__ __forceinline__ double wave_scan_d(double v) { return wave_scan(v); }
+
+// Reductions over lanes 0-7 (quad permutes, then the half-row mirror): every one of lanes
+// 0-7 ends with the combination of all eight, read from lane 0.
+template <typename T, typename F>
+__device__ __forceinline__ T lane8_reduce(T v, F &&op) {
+    v = op(v, dpp_move<0xB1, 0xF>(v));
+    v = op(v, dpp_move<0x4E, 0xF>(v));
+    v = op(v, dpp_move<0x141, 0xF>(v));
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, 0);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 0);
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
 }
 
 // (value desc, index asc) with index < 0 meaning "none": the greedy combine.
@@ -299,6 +334,18 @@ __device__ __forceinline__ double rng_unit(uint64_t &st) {
 }
 
 // sample.c:83-92: append, or overwrite the oldest once the ring is full.
+// With the row's history length and head already loaded (len, head).
+__device__ __forceinline__ void ring_record_at(int32_t *ring, int32_t *hlen, int32_t *hhead,
+                                               int cap, int id, int len, int head) {
+    if (cap <= 0) return;
+    if (len < cap) {
+        ring[(head + len) % cap] = id;
+        *hlen = len + 1;
+    } else {
+        ring[head] = id;
+        *hhead = (head + 1) % cap;
+    }
+}
 __device__ __forceinline__ void ring_record(int32_t *ring, int32_t *hlen, int32_t *hhead,
                                             int cap, int id) {
     if (cap <= 0) return;
@@ -987,6 +1034,7 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
     const float thr = msc - 30.0f;
     if (!isfinite(msc) || t.cflag || t.total > WAVE_CAND) return 1;
     uint64_t rs = st.rng[row];                     // in flight during the selection
+    const int hl = st.hlen[row], hh = st.hhead[row];
     uint32_t k[4];
     int idv[4];
     bool valid[4];
@@ -1056,7 +1104,7 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
     if (lane == 0) {
         int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
         st.rng[row] = rs;
-        ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
+        ring_record_at(ring, st.hlen + row, st.hhead + row, P.ring_cap, id, hl, hh);
         out[row] = id;
         if (diag) {
             d.id = id;

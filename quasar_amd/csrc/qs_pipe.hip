@@ -611,23 +611,22 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
             wave_best(bv, bi);
             if (lane == 0) { pl.gbv = bv; pl.gbi = bi; pl.tot.maxl = mx; }
         } else {
+            // one value per part in lanes 0-7: eight-lane reductions and scan
+            static_assert(PARTS == 8, "lanes 0-7 hold the parts");
             double ps = have ? ld_dev(&sc.psum[l0 + lane]) : 0.0;
             int pc = have ? ld_dev(&sc.pcnt[l0 + lane]) : 0;
             int cc = have ? ld_dev(&sc.ccnt[l0 + lane]) : 0;
             int cf = have ? ld_dev(&sc.cflag[l0 + lane]) : 0;
             uint32_t cr = have ? ld_dev(&sc.crej[l0 + lane]) : 0u;
-            ps = wave_sum_d(ps);
-            pc = wave_sum_i(pc);
-            cf = wave_or_i(cf);
-            cr = wave_max_u(cr);
-            const uint32_t rmx = wave_max_u(have ? ld_dev(&sc.rowmax[(int64_t)row * PARTS + lane]) : 0u);
-            int incl = cc;
-            for (int o = 1; o < 64; o <<= 1) {
-                const int t = __shfl_up(incl, o, 64);
-                if (lane >= o) incl += t;
-            }
+            uint32_t rk = have ? ld_dev(&sc.rowmax[(int64_t)row * PARTS + lane]) : 0u;
+            ps = lane8_reduce(ps, [](double x, double y) { return x + y; });
+            pc = lane8_reduce(pc, [](int x, int y) { return x + y; });
+            cf = lane8_reduce(cf, [](int x, int y) { return x | y; });
+            cr = lane8_reduce(cr, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+            const uint32_t rmx = lane8_reduce(rk, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+            const int incl = wave_scan(cc);
             if (have) pl.offs[lane] = incl - cc;
-            if (lane == 63) pl.offs[PARTS] = incl;
+            if (lane == PARTS - 1) pl.offs[PARTS] = incl;
             if (lane == 0) {
                 pl.tot.maxl = key2f(rmx);
                 pl.tot.sum = ps;
