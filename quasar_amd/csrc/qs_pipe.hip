@@ -157,19 +157,26 @@ __device__ __forceinline__ void set_cfg(PartCfg &c, const qs_row_param &P, bool 
 // (size 0), return zeros without a memory access.  Every stage issues the same UP loads,
 // so each wave's memory counter names exactly the loads a use waits for.
 constexpr int BUF_WORD3 = 0x00020000;    // raw buffer, 32-bit data format
+struct PartLoad {                        // the loads of one part (see issue_loads)
+    __amdgpu_buffer_rsrc_t rs;
+    int off;
+    __device__ PartLoad(const PipeArgs &a, int row, bool live, const Geo &g) {
+        const float *base = a.logits + (live ? (int64_t)row * a.stride + 4 * (int64_t)g.c_lo : 0);
+        const int bytes = live ? (g.c_hi - g.c_lo) * 16 : 0;
+        rs = __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, bytes, BUF_WORD3);
+        off = data_tid() * 16;
+    }
+    __device__ float4 load(int u) const {        // u's offset in the scalar offset
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, u * DT * 16, 0);
+        return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                           __uint_as_float(v[3]));
+    }
+};
 __device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a, int row,
                                             bool live, const Geo &g) {
-    const float *base = a.logits + (live ? (int64_t)row * a.stride + 4 * (int64_t)g.c_lo : 0);
-    const int bytes = live ? (g.c_hi - g.c_lo) * 16 : 0;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, bytes, BUF_WORD3);
-    const int off = data_tid() * 16;
+    const PartLoad nl(a, row, live, g);
 #pragma unroll
-    for (int u = 0; u < UP; ++u) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * DT * 16, 0, 0);
-        buf[u] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]),
-                             __uint_as_float(v[2]), __uint_as_float(v[3]));
-    }
+    for (int u = 0; u < UP; ++u) buf[u] = nl.load(u);
 }
 
 // Data waves: penalty (sample.c:118-128) and each thread's max key (the control wave takes
@@ -251,14 +258,17 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], float &mn, cons
 // above the threshold skips the candidate test.
 constexpr float X_OUT = -32.0f;
 
-__device__ __forceinline__ void sum_part(const float4 (&buf)[UP], float mn, const Geo &g,
-                                         const PartCfg &cf, uint32_t *ckey, int32_t *cid,
-                                         uint32_t maxkey, uint32_t th, PipeLds &pl, int par) {
+__device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const PartLoad &nl,
+                                         bool live, const Geo &g, const PartCfg &cf,
+                                         uint32_t *ckey, int32_t *cid, uint32_t maxkey,
+                                         uint32_t th, PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float inv_t = cf.inv_t;
     const float msc = key2f(maxkey) * inv_t;
     const float thr = msc - 30.0f;
-    if ((cf.flags & CFG_GREEDY) || !isfinite(msc)) return;   // decided in the epilogue
+    // greedy rows and rows without a finite maximum are decided in the epilogue: only the
+    // next part's loads
+    const bool work = live && !(cf.flags & CFG_GREEDY) && isfinite(msc);
     // candidates: every w >= key2f(th), tested as w*inv_t >= key2f(th)*inv_t (monotone in
     // w, so a superset; rejected logits stay below th)
     const float ths = key2f(th) * inv_t;
@@ -266,11 +276,12 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], float mn, cons
     const bool wave_in = __ballot(!(mn * inv_t >= thr)) == 0ull;   // NaN is not in
     float xo = X_OUT;
     asm volatile("" : "+v"(xo));                    // a register, selected before the exp
-    double acc0 = 0.0, acc1 = 0.0;
+    double acc = 0.0;
     int cnt = 0;
     const int dt = data_tid();
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
+      if (work) {
         const int c = g.c_lo + u * DT + dt;
         const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
         float sc[4];
@@ -295,10 +306,10 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], float mn, cons
 #pragma unroll
             for (int k = 0; k < 4; ++k) xa[k] = sc[k] - msc;
             qs_expf4_window(xa, e, xtab);
-            acc0 += (double)e[0];
-            acc1 += (double)e[1];
-            acc0 += (double)e[2];
-            acc1 += (double)e[3];
+            acc += (double)e[0];
+            acc += (double)e[1];
+            acc += (double)e[2];
+            acc += (double)e[3];
         } else if (in[0] | in[1] | in[2] | in[3]) {
             float xa[4], e[4];
             bool ok[4];
@@ -310,10 +321,10 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], float mn, cons
             qs_expf4_window(xa, e, xtab);
 #pragma unroll
             for (int k = 0; k < 4; ++k) e[k] = ok[k] ? e[k] : 0.0f;
-            acc0 += (double)e[0];
-            acc1 += (double)e[1];
-            acc0 += (double)e[2];
-            acc1 += (double)e[3];
+            acc += (double)e[0];
+            acc += (double)e[1];
+            acc += (double)e[2];
+            acc += (double)e[3];
         }
         if (__ballot(sc[0] >= ths) | __ballot(sc[1] >= ths) | __ballot(sc[2] >= ths) |
             __ballot(sc[3] >= ths)) {
@@ -328,8 +339,14 @@ __device__ __forceinline__ void sum_part(const float4 (&buf)[UP], float mn, cons
                 }
             }
         }
+      }
+        // the next part's float4 u, as soon as this one is done (kept after this float4's
+        // work: hoisted, the load would need registers of its own)
+        asm volatile("" ::: "memory");
+        buf[u] = nl.load(u);
     }
-    const double sa = wave_sum_d(acc0 + acc1);
+    if (!work) return;
+    const double sa = wave_sum_d(acc);
     if (lane == 0) {
         pl.wsum[par][wv] = sa;
         pl.wcnt[par][wv] = cnt;        // the wave's count (sum of ballot popcounts)
@@ -687,11 +704,10 @@ __device__ __forceinline__ void data_stage(float4 (&cur)[UP], float mcur, float4
     // data wavefront lowers its priority as it gets through the stage, so the ones behind
     // catch up and the SIMD keeps several wavefronts to switch between until the end.
     __builtin_amdgcn_s_setprio(2);
-    if (v0)
-        sum_part(cur, mcur, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP, pl.maxkey[s % 3],
-                 pl.theta[s & 3], pl, p0);
+    const PartLoad nl(a, r3, v3, g);              // part s+3, into `cur` as it is summed
+    sum_part(cur, mcur, nl, v0, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP,
+             pl.maxkey[s % 3], pl.theta[s & 3], pl, p0);
     __builtin_amdgcn_s_setprio(1);
-    issue_loads(cur, a, r3, v3, g);
     if (v2) complete_part(ld, mld, g, bm + ((s + 2) % 3) * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
     __builtin_amdgcn_s_setprio(0);
 }
