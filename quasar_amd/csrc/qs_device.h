@@ -1014,6 +1014,15 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// A row's generator state and history position, loaded ahead of its decision.
+struct RowHist {
+    uint64_t rng;
+    int len, head;
+};
+__device__ __forceinline__ RowHist row_hist(const RowState &st, int row) {
+    return RowHist{st.rng[row], st.hlen[row], st.hhead[row]};
+}
+
 // decide_row's decision for one row by one wavefront, in registers: a threshold keeping
 // the K largest candidate keys and at most 64 (a bit-serial ballot bracket), exact p per
 // lane, a 64-lane bitonic sort by (p desc, id asc), the proof of the prefix and
@@ -1027,14 +1036,14 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
                                                const uint32_t *keys, const int32_t *ids,
                                                uint64_t *scratch, const uint64_t *tab,
                                                const RowState &st, int32_t *out,
-                                               qs_pick_diag *diag) {
+                                               qs_pick_diag *diag, const RowHist &h) {
     const int lane = threadIdx.x & 63;
     const float inv_t = P.inv_t;
     const float msc = t.maxl * inv_t;
     const float thr = msc - 30.0f;
     if (!isfinite(msc) || t.cflag || t.total > WAVE_CAND) return 1;
-    uint64_t rs = st.rng[row];                     // in flight during the selection
-    const int hl = st.hlen[row], hh = st.hhead[row];
+    uint64_t rs = h.rng;
+    const int hl = h.len, hh = h.head;
     uint32_t k[4];
     int idv[4];
     bool valid[4];
@@ -1130,9 +1139,10 @@ __device__ __forceinline__ void decide_row_fast(int row, const qs_row_param &P, 
                                                 FullLds<NT> &fl, const float *x, int V,
                                                 const RowState &st, const Scratch &sc,
                                                 int32_t *out, qs_pick_diag *diag,
-                                                int fixed_slot) {
+                                                int fixed_slot, const RowHist *pre = nullptr) {
     if (threadIdx.x < 64) {
-        const int status = decide_row_wave(row, P, t, keys, ids, srt, dl.tab, st, out, diag);
+        const RowHist h = pre ? *pre : row_hist(st, row);   // loaded by the caller, or now
+        const int status = decide_row_wave(row, P, t, keys, ids, srt, dl.tab, st, out, diag, h);
         if (threadIdx.x == 0) dl.sh[7] = status;
     }
     __syncthreads();

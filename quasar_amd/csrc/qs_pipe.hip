@@ -596,6 +596,8 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
     const RowState &st = a.st;
     const Scratch &sc = a.sc;
     const qs_row_param P = st.prm[row];
+    RowHist hist{0ull, 0, 0};                        // the decision's, in flight meanwhile
+    if (tid < 64) hist = row_hist(st, row);
     if (tid == 0) {
         int it = 0;
         while (ld_dev(&sc.done[row]) < PARTS) {
@@ -681,7 +683,7 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
         }
         __syncthreads();
         decide_row_fast<NT>(row, P, t, FCAP, keys, ids, srt, pl.dl, fl, x, a.vocab, st, sc,
-                            a.out, a.diag, slot);
+                            a.out, a.diag, slot, &hist);
     }
     __syncthreads();
     if (tid < PARTS) st_dev(&sc.rowmax[(int64_t)row * PARTS + tid], 0u);   // ready for the
