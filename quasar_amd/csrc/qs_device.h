@@ -97,16 +97,28 @@ __device__ __forceinline__ int wave_or_i(int v) {
     return wave_reduce(v, [](int a, int b) { return a | b; });
 }
 
-// The value of lane (lane ^ S): DPP for S = 1, 2 (quad permutes) and 8 (a rotation by 8
-// within each row of 16 lanes), ds_swizzle in bit mode (xor within 32 lanes) for 4 and 16,
-// ds_bpermute for 32.
+// The value of lane (lane ^ S), in VALU moves only: DPP for S = 1, 2 (quad permutes) and
+// 8 (a rotation by 8 within each row of 16 lanes); for 4, the row shifts by 4 up and down
+// and a select by lane bit 2; for 16 and 32, v_permlane16_swap / v_permlane32_swap (each
+// lane receives the pair {v[lane & ~S], v[lane | S]}) and a select by lane bit.
 template <int S>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    const bool up = (threadIdx.x & S) != 0;
     if constexpr (S == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
     else if constexpr (S == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
     else if constexpr (S == 8) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
-    else if constexpr (S == 4 || S == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (S << 10));
-    else return (uint32_t)__shfl_xor((int)v, S, 64);
+    else if constexpr (S == 4) {
+        const uint32_t fwd = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);  // row_shl:4
+        const uint32_t bwd = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+        return up ? bwd : fwd;
+    } else if constexpr (S == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return up ? p[0] : p[1];
+    } else {
+        static_assert(S == 32, "lane distances 1, 2, 4, 8, 16, 32");
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return up ? p[0] : p[1];
+    }
 }
 template <int S>
 __device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
