@@ -352,8 +352,10 @@ def test_mode_equals_split(qa, oracle, mode, name, B, picks):
 @pytest.mark.parametrize("mode", sorted(MODES))
 def test_mode_mixed_rows(qa, oracle, mode):
     """A 64-row batch at the full vocabulary where each row has its own parameters
-    (greedy rows, top-k off, penalties, degenerate rows), through the pipelined or the
-    one-pass kernel, against the CPU restatement row by row over three picks."""
+    (greedy rows, top-k off, penalties, degenerate rows: ties, +inf, all -inf, NaN runs,
+    a single NaN, signalling NaNs, a NaN in the last part's tail, a signed-zero max, one
+    finite logit), through the pipelined or the one-pass kernel, against the CPU
+    restatement row by row over three picks."""
     rng = np.random.default_rng(21)
     B, V = 64, 151936
     x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
@@ -361,6 +363,16 @@ def test_mode_mixed_rows(qa, oracle, mode):
     x[6, 1000] = np.float32(np.inf)                # +inf max: degenerate window
     x[7, :] = np.float32(-np.inf)                  # all -inf
     x[8, ::3] = np.float32(np.nan)
+    x[9, 77777] = np.float32(np.nan)               # one NaN
+    snan = np.array([0x7F800001, 0xFF800001, 0x7FA00000], dtype=np.uint32).view(np.float32)
+    x[10, [int(np.argmax(x[10])), 3, 151935]] = snan   # signalling NaNs, one at the max
+    x[11, V - 3] = np.float32(np.nan)              # NaN in the last part's tail
+    x[11, V - 1] = np.float32(9.0)
+    x[12, :] = -np.abs(x[12, :]) - np.float32(1.0)  # the max is a signed zero
+    x[12, 100] = np.float32(-0.0)
+    x[12, 200] = np.float32(0.0)
+    x[13, :] = np.float32(-np.inf)                 # one finite logit
+    x[13, 4242] = np.float32(-3.0)
     buf = qa.DeviceBuffer.from_array(x)
     per_row, hists = [], []
     for r in range(B):
