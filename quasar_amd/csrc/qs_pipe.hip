@@ -258,6 +258,16 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], float &mn, cons
 // above the threshold skips the candidate test.
 constexpr float X_OUT = -32.0f;
 
+// The largest of four products w * inv_t (never signalling NaNs: the product quiets them)
+// with quiet NaNs ignored, as v_max3_f32 does without the operand canonicalisation that
+// fmaxf implies: a float4 holding a candidate always passes the test below.
+__device__ __forceinline__ float max4q(const float (&v)[4]) {
+    float m;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(m) : "v"(v[0]), "v"(v[1]), "v"(v[2]));
+    asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(m), "v"(v[3]));
+    return m;
+}
+
 __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const PartLoad &nl,
                                          bool live, const Geo &g, const PartCfg &cf,
                                          uint32_t *ckey, int32_t *cid, uint32_t maxkey,
@@ -274,6 +284,11 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
     const float ths = key2f(th) * inv_t;
     const uint64_t *xtab = pl.xtab;
     const bool wave_in = __ballot(!(mn * inv_t >= thr)) == 0ull;   // NaN is not in
+    // no lane whose max key (complete_part's, still in its slot) reaches th: no candidate
+    // (a logit below th that the scaled test would also take is not needed: the part's
+    // rejected bound is th - 1)
+    const bool wave_cand =
+        work && __ballot(pl.lmax[par][(wv - 1) * LM_STRIDE + lane] >= th) != 0ull;
     float xo = X_OUT;
     asm volatile("" : "+v"(xo));                    // a register, selected before the exp
     double acc = 0.0;
@@ -281,12 +296,31 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
     const int dt = data_tid();
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
-      if (work) {
-        const int c = g.c_lo + u * DT + dt;
-        const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
         float sc[4];
+        if (work) {
+            const int c = g.c_lo + u * DT + dt;
+            const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) sc[k] = w[k] * inv_t;
+            for (int k = 0; k < 4; ++k) sc[k] = w[k] * inv_t;
+            if (wave_cand && __ballot(max4q(sc) >= ths)) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (sc[k] >= ths) {
+                        const int pos = atomicAdd(&pl.ncand[par], 1);
+                        if (pos < PCAP) {
+                            ckey[pos] = f2key(w[k]);
+                            cid[pos] = 4 * c + k;
+                        }
+                    }
+                }
+            }
+        }
+        // the next part's float4 u as soon as this one's logits are no longer needed (the
+        // exp below works on sc); kept here: hoisted, the load would need registers of its
+        // own
+        asm volatile("" ::: "memory");
+        buf[u] = nl.load(u);
+        if (!work) continue;
         uint64_t in[4];
         bool all;
         if (u < UP - 1 && wave_in) {                // every lane's four in the window
@@ -326,24 +360,6 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
             acc += (double)e[2];
             acc += (double)e[3];
         }
-        if (__ballot(sc[0] >= ths) | __ballot(sc[1] >= ths) | __ballot(sc[2] >= ths) |
-            __ballot(sc[3] >= ths)) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (sc[k] >= ths) {
-                    const int pos = atomicAdd(&pl.ncand[par], 1);
-                    if (pos < PCAP) {
-                        ckey[pos] = f2key(w[k]);
-                        cid[pos] = 4 * c + k;
-                    }
-                }
-            }
-        }
-      }
-        // the next part's float4 u, as soon as this one is done (kept after this float4's
-        // work: hoisted, the load would need registers of its own)
-        asm volatile("" ::: "memory");
-        buf[u] = nl.load(u);
     }
     if (!work) return;
     const double sa = wave_sum_d(acc);
