@@ -54,6 +54,7 @@ constexpr int DT = NT - 64;          // data threads (waves 1..15)
 constexpr int PARTS = 8;             // parts per row
 constexpr int UP = 5;                // float4 per data thread per part
 constexpr int PCAP = 512;            // candidates per part (<= Scratch::ccap)
+constexpr int WCAP = 32;             // candidates per data wave in LDS (NDW * WCAP <= PCAP)
 constexpr int FCAP = 4096;           // candidates gathered per row in the epilogue
 constexpr int NDW = NWV - 1;         // data waves
 // Thread max keys of data wave j start at j*LM_STRIDE: an odd stride puts the 16 keys
@@ -99,7 +100,8 @@ struct PipeLds {
     int wbi[2][NWV];
     double wsum[2][NWV];             // per-wave partial sums of a summed part
     int wcnt[2][NWV];                // per-wave window counts
-    int ncand[2];                    // candidates in the LDS lists
+    int wcand[2][NWV];               // candidates each data wave found (its LDS list holds
+                                     // the first WCAP of them)
     uint32_t maxkey[3];              // row max keys (by part index mod 3)
     uint32_t theta[4];               // candidate threshold keys (by part index mod 4)
     PartCfg cfg[4];                  // by part index mod 4
@@ -276,6 +278,7 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
     const float inv_t = cf.inv_t;
     const float msc = key2f(maxkey) * inv_t;
     const float thr = msc - 30.0f;
+    static_assert(NDW * WCAP <= PCAP, "every wave's list fits the part's");
     // greedy rows and rows without a finite maximum are decided in the epilogue: only the
     // next part's loads
     const bool work = live && !(cf.flags & CFG_GREEDY) && isfinite(msc);
@@ -292,7 +295,9 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
     float xo = X_OUT;
     asm volatile("" : "+v"(xo));                    // a register, selected before the exp
     double acc = 0.0;
-    int cnt = 0;
+    int cnt = 0, wn = 0;                            // window count; candidates found
+    uint32_t *wk = ckey + (wv - 1) * WCAP;         // this wave's candidate list
+    int32_t *wi = cid + (wv - 1) * WCAP;
     const int dt = data_tid();
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
@@ -304,14 +309,16 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
             for (int k = 0; k < 4; ++k) sc[k] = w[k] * inv_t;
             if (wave_cand && __ballot(max4q(sc) >= ths)) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    if (sc[k] >= ths) {
-                        const int pos = atomicAdd(&pl.ncand[par], 1);
-                        if (pos < PCAP) {
-                            ckey[pos] = f2key(w[k]);
-                            cid[pos] = 4 * c + k;
-                        }
+                for (int k = 0; k < 4; ++k) {            // positions by ballot prefix: no
+                    const bool hit = sc[k] >= ths;       // atomics, nothing waited for
+                    const uint64_t m = __ballot(hit);
+                    if (m == 0ull) continue;
+                    const int pos = wn + lane_prefix(m);
+                    if (hit && pos < WCAP) {
+                        wk[pos] = f2key(w[k]);
+                        wi[pos] = 4 * c + k;
                     }
+                    wn += __popcll(m);
                 }
             }
         }
@@ -366,6 +373,7 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
     if (lane == 0) {
         pl.wsum[par][wv] = sa;
         pl.wcnt[par][wv] = cnt;        // the wave's count (sum of ballot popcounts)
+        pl.wcand[par][wv] = wn;
     }
 }
 
@@ -577,14 +585,22 @@ __device__ __forceinline__ bool control_store(const PipeArgs &a, int row, const 
     if (cf.flags & CFG_GREEDY) return false;      // published with its best already
     const int li = row * PARTS + g.part;
     const bool live = isfinite(key2f(maxkey) * cf.inv_t);
-    const int nc = pl.ncand[par];
-    const int n = live ? min(nc, PCAP) : 0;
-    const int ovf = live && nc > PCAP;
+    // the data waves' lists, one count per lane, concatenated in wave order: lane 4j+q
+    // copies entries q, q+4, ... of data wave j's list
+    const int cw = (live && lane < NDW) ? pl.wcand[par][lane + 1] : 0;
+    const int cwc = min(cw, WCAP);
+    const int incl = wave_scan(cwc);
+    const int n = __builtin_amdgcn_readlane(incl, NDW - 1);
+    const int ovf = __ballot(cw > WCAP) != 0ull;   // a list overflowed: incomplete
     uint32_t *gk = a.sc.ckey + (int64_t)li * PCAP;
     int32_t *gi = a.sc.cid + (int64_t)li * PCAP;
-    for (int j = lane; j < n; j += 64) {
-        st_dev(&gk[j], ckey[j]);
-        st_dev(&gi[j], cid[j]);
+    {
+        const int j = (lane >> 2) & 15;            // lanes 60-63: lane 15's count, 0
+        const int cnt_j = __shfl(cwc, j, 64), off_j = __shfl(incl - cwc, j, 64);
+        for (int i = lane & 3; i < cnt_j; i += 4) {
+            st_dev(&gk[off_j + i], ckey[j * WCAP + i]);
+            st_dev(&gi[off_j + i], cid[j * WCAP + i]);
+        }
     }
     // the data waves' partial sums and window counts, one per lane (every data wave wrote
     // its own when the part is live)
@@ -598,7 +614,6 @@ __device__ __forceinline__ bool control_store(const PipeArgs &a, int row, const 
         st_dev(&a.sc.cflag[li], ovf);
         st_dev(&a.sc.crej[li], (live && th > KEY_NEG_INF) ? th - 1u : 0u);
     }
-    if (lane == 0) pl.ncand[par] = 0;
     return true;
 }
 __device__ __forceinline__ void control_release(const PipeArgs &a, int row) {
@@ -786,7 +801,6 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     uint32_t *bm = dyn;                              // [3][bm_words], part p at p mod 3
     uint32_t *ckey = dyn + 3 * g.bm_words;           // [2][PCAP]
     int32_t *cid = (int32_t *)(ckey + 2 * PCAP);     // [2][PCAP]
-    if (tid == 0) pl.ncand[0] = pl.ncand[1] = 0;
 
     // prologue: parts 0 and 1 completed, part 0's row max known (exchanged while part 1
     // is completed), part 2 loading and its bitmap built.  Data and control waves then run loops of their own (the branch is on
