@@ -812,12 +812,11 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     if (wave != 0) {
         float4 B0[UP], B1[UP], B2[UP];
         float M0 = 0.0f, M1 = 0.0f, M2 = 0.0f;  // thread minima of the parts in B0..B2
-        __syncthreads();                         // the control wave's fetches go first
-        issue_loads(B0, a, r0, t0, g);
-        for (int j = tid - 64; j < QS_EXPF_XTAB_N; j += DT) pl.xtab[j] = qs_expf_xtab_entry(pl.dl.tab, j);
+        issue_loads(B0, a, r0, t0, g);           // at once, beside the control wave's fetches
         __syncthreads();                         // every wave's part 0 ahead of part 1
         issue_loads(B1, a, r1, t1, g);
-        __syncthreads();
+        for (int j = tid - 64; j < QS_EXPF_XTAB_N; j += DT) pl.xtab[j] = qs_expf_xtab_entry(pl.dl.tab, j);
+        __syncthreads();                         // part 0's bitmap and settings
         if (t0) complete_part(B0, M0, g, bm, pl.cfg[0], pl, 0);
         __syncthreads();                         // part 0's max is exchanged meanwhile
         issue_loads(B2, a, r2, t2, g);
@@ -834,7 +833,7 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         // the control wave's steps are on every stage's critical path: it issues ahead of
         // the data wavefronts that share its SIMD
         __builtin_amdgcn_s_setprio(3);
-        // every row fetch of the prologue in flight before the data waves issue theirs
+        // the row fetches of the prologue, issued as the data waves issue part 0's loads
         const bool t3 = task_valid(a, 3, g, w);
         RowFetch f0, f1, f2, rp;
         if (t0) f0 = fetch_row(a, r0);
@@ -843,16 +842,15 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         if (t3) rp = fetch_row(a, task_row(3, w, g.rps));
         if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];   // after the fetches
         __syncthreads();
-        __syncthreads();
         if (t0) {
             bitmap_build(bm, f0, a, r0, g);
             set_cfg(pl.cfg[0], f0.param(), row_pen(f0));
         }
+        __syncthreads();                             // part 0 is completed meanwhile
         if (t1) {
             bitmap_build(bm + g.bm_words, f1, a, r1, g);
             set_cfg(pl.cfg[1], f1.param(), row_pen(f1));
         }
-        __syncthreads();
         if (t2) {                                    // used from stage 0 on
             bitmap_build(bm + 2 * g.bm_words, f2, a, r2, g);
             set_cfg(pl.cfg[2], f2.param(), row_pen(f2));
