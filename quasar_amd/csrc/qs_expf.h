@@ -83,15 +83,15 @@ QS_EXPF_FN float qs_expf_core(float x, const uint64_t *tab) {
  * SHIFT (XOFF a multiple of 32; both in the binade [2^52, 2^53), where adding rounds to an
  * integer of the same parity, hence the same tie-breaking) leaves r unchanged and makes the
  * low word k + XOFF, which lies in [0, XOFF] for k in [-XOFF, 0].  Entry j of the extended
- * table is T[j & 31] with XOFF >> 5 taken off its exponent field, so adding (k + XOFF) << 15
- * to its high word gives the same bits as adding k << 15 to T[k & 31]'s: the results equal
- * qs_expf_core's bit for bit, one mask fewer per element. */
+ * table is the scale itself for k = j - XOFF: T[k & 31] plus k << 47 (modulo 2^64), the bits
+ * qs_expf_core forms per element, so the results equal qs_expf_core's bit for bit with one
+ * mask and one add fewer per element. */
 #define QS_EXPF_XOFF 1536
 #define QS_EXPF_XTAB_N (QS_EXPF_XOFF + 1)
 #define QS_EXPF_XSHIFT (QS_EXPF_SHIFT + QS_EXPF_XOFF)
 
 QS_EXPF_FN uint64_t qs_expf_xtab_entry(const uint64_t *tab, int j) {
-    return tab[j & (QS_EXPF_TAB_N - 1)] - ((uint64_t)QS_EXPF_XOFF << 47);
+    return tab[j & (QS_EXPF_TAB_N - 1)] + ((uint64_t)(int64_t)(j - QS_EXPF_XOFF) << 47);
 }
 
 QS_EXPF_FN float qs_expf_window(float x, const uint64_t *xtab) {
@@ -100,14 +100,7 @@ QS_EXPF_FN float qs_expf_window(float x, const uint64_t *xtab) {
     uint32_t klo = (uint32_t)qs_d2u(kd);
     kd = kd - QS_EXPF_XSHIFT;
     double r = __builtin_fma(QS_EXPF_INVLN2N, xd, -kd);
-    const uint64_t te = xtab[klo];
-    uint32_t thi = (uint32_t)(te >> 32);
-#ifdef __HIP_DEVICE_COMPILE__
-    asm("v_lshl_add_u32 %0, %1, 15, %0" : "+v"(thi) : "v"(klo));
-#else
-    thi += klo << 15;
-#endif
-    double s = qs_u2d(((uint64_t)thi << 32) | (uint32_t)te);
+    double s = qs_u2d(xtab[klo]);
     double z = __builtin_fma(QS_EXPF_C0, r, QS_EXPF_C1);
     double r2 = r * r;
     double y = __builtin_fma(QS_EXPF_C2, r, 1.0);
@@ -119,15 +112,20 @@ QS_EXPF_FN float qs_expf_window(float x, const uint64_t *xtab) {
 #ifdef __HIPCC__
 /* qs_expf_window on four arguments at once, in phases (argument reductions, then the four
  * table reads, then the polynomials, then the scaling), so the table reads are in flight
- * together instead of each waiting out its own latency.  Same operations, same results. */
+ * together instead of each waiting out its own latency.  Same operations, same results.
+ * A caller with a loop passes the shifter and C1 (the default values) from registers that
+ * stay live across it: an operation has room for one scalar operand besides, and a
+ * constant would be copied into a vector register for every call. */
 __device__ static inline void qs_expf4_window(const float (&x)[4], float (&e)[4],
-                                              const uint64_t *xtab) {
+                                              const uint64_t *xtab,
+                                              double kshift = QS_EXPF_XSHIFT,
+                                              double c1 = QS_EXPF_C1) {
     double r[4];
     uint32_t klo[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const double xd = (double)x[k];
-        double kd = __builtin_fma(QS_EXPF_INVLN2N, xd, QS_EXPF_XSHIFT);
+        double kd = __builtin_fma(QS_EXPF_INVLN2N, xd, kshift);
         klo[k] = (uint32_t)qs_d2u(kd);
         kd = kd - QS_EXPF_XSHIFT;
         r[k] = __builtin_fma(QS_EXPF_INVLN2N, xd, -kd);
@@ -138,22 +136,13 @@ __device__ static inline void qs_expf4_window(const float (&x)[4], float (&e)[4]
     double y[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const double z = __builtin_fma(QS_EXPF_C0, r[k], QS_EXPF_C1);
+        const double z = __builtin_fma(QS_EXPF_C0, r[k], c1);
         const double r2 = r[k] * r[k];
         double t = __builtin_fma(QS_EXPF_C2, r[k], 1.0);
         y[k] = __builtin_fma(z, r2, t);
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        uint32_t thi = (uint32_t)(te[k] >> 32);
-#ifdef __HIP_DEVICE_COMPILE__
-        asm("v_lshl_add_u32 %0, %1, 15, %0" : "+v"(thi) : "v"(klo[k]));
-#else
-        thi += klo[k] << 15;
-#endif
-        const double sc = qs_u2d(((uint64_t)thi << 32) | (uint32_t)te[k]);
-        e[k] = (float)(y[k] * sc);
-    }
+    for (int k = 0; k < 4; ++k) e[k] = (float)(y[k] * qs_u2d(te[k]));
 }
 #endif
 

@@ -294,6 +294,8 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
         work && __ballot(pl.lmax[par][(wv - 1) * LM_STRIDE + lane] >= th) != 0ull;
     float xo = X_OUT;
     asm volatile("" : "+v"(xo));                    // a register, selected before the exp
+    double kshift = QS_EXPF_XSHIFT, c1 = QS_EXPF_C1;
+    asm volatile("" : "+v"(kshift), "+v"(c1));      // in registers for the whole loop
     double acc = 0.0;
     int cnt = 0, wn = 0;                            // window count; candidates found
     uint32_t *wk = ckey + (wv - 1) * WCAP;         // this wave's candidate list
@@ -346,7 +348,7 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
             float xa[4], e[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) xa[k] = sc[k] - msc;
-            qs_expf4_window(xa, e, xtab);
+            qs_expf4_window(xa, e, xtab, kshift, c1);
             acc += (double)e[0];
             acc += (double)e[1];
             acc += (double)e[2];
@@ -359,7 +361,7 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
                 ok[k] = sc[k] >= thr;
                 xa[k] = ok[k] ? sc[k] - msc : xo;
             }
-            qs_expf4_window(xa, e, xtab);
+            qs_expf4_window(xa, e, xtab, kshift, c1);
 #pragma unroll
             for (int k = 0; k < 4; ++k) e[k] = ok[k] ? e[k] : 0.0f;
             acc += (double)e[0];
