@@ -46,18 +46,20 @@ __device__ __forceinline__ int lane_prefix(uint64_t m) {
 // other wavefronts' LDS traffic): pairs and quads by quad permutes, 8 and 16 lanes by the
 // half-row and row mirrors, then row 1 (3) takes row 0's (2's) lane 15 and rows 2-3 take
 // lane 31; lane 63 ends with the whole wavefront and is broadcast.  The combination order
-// is fixed by lane positions, so double sums do not depend on timing.
+// is fixed by lane positions, so double sums do not depend on timing.  Rows a broadcast
+// does not write keep undefined values (a move into a fresh register, no copy first): only
+// lane 63's result is read, and it never combines them.
 template <int CTRL, int ROWS, typename T>
 __device__ __forceinline__ T dpp_move(T x) {
     static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
     if constexpr (sizeof(T) == 4) {
         const int b = __builtin_bit_cast(int, x);
-        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(b, b, CTRL, ROWS, 0xF, false));
+        return __builtin_bit_cast(T, __builtin_amdgcn_mov_dpp(b, CTRL, ROWS, 0xF, false));
     } else {
         const uint64_t u = __builtin_bit_cast(uint64_t, x);
         const int lo = (int)(uint32_t)u, hi = (int)(uint32_t)(u >> 32);
-        const uint32_t rlo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWS, 0xF, false);
-        const uint32_t rhi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWS, 0xF, false);
+        const uint32_t rlo = (uint32_t)__builtin_amdgcn_mov_dpp(lo, CTRL, ROWS, 0xF, false);
+        const uint32_t rhi = (uint32_t)__builtin_amdgcn_mov_dpp(hi, CTRL, ROWS, 0xF, false);
         return __builtin_bit_cast(T, ((uint64_t)rhi << 32) | rlo);
     }
 }
