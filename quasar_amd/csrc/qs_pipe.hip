@@ -10,21 +10,19 @@
 //
 // Wave 0 is the control wave and never loads logits; waves 1-15 (960 threads, UP float4
 // each) hold data.  Three register buffers rotate: the part being summed (s), the next
-// part, already penalised and published (s+1), and the part after that, loading (s+2).
-// Per stage:
+// part, already penalised and published (s+1), and the part after that (s+2), loaded as
+// part s-1 was summed.  Per stage, between two barriers:
 //
-//   data waves                              control wave
-//   sum(s): w*inv_t, window, libm-equal     publish the max of part s+1 (completed last
-//   expf, double partial sums, candidates   stage); history bitmap for part s+2
-//   at or above threshold(s)
-//   -------------------------------------- barrier --------------------------------------
-//   complete(s+2): penalty, part max,       store part s's sums and candidates; read the
-//   threshold(s+2) (per-wave ballot select  row max of part s+1, published half a stage
-//   over lane maxima); loads of part s+3    earlier by all eight partners
-//   -------------------------------------- barrier --------------------------------------
+//   data waves                                control wave
+//   sum(s): w*inv_t, window, libm-equal       publish the max of part s+1 (completed last
+//   expf, double partial sums, candidates     stage); store part s-1's sums and
+//   at or above threshold(s); loads of part   candidates; part s+1's candidate threshold;
+//   s+3 into the summed registers             history bitmap of part s+3; read the row
+//   complete(s+2): penalty, thread max and    max of part s+1 (all eight partners
+//   min                                       published it about the same time)
 //
-// so the row-max exchange has half a stage to travel, the stores overlap the data waves'
-// work, and a wave's memory counter never covers another wave's loads.  After the last
+// so the row-max exchange overlaps the control wave's other work, the stores overlap the
+// data waves' and a wave's memory counter never covers another wave's loads.  After the last
 // stage each workgroup finishes rows r = w (mod G) with decide_row_fast, using its own
 // full-window scratch slot.
 //
@@ -105,6 +103,8 @@ struct PipeLds {
     uint32_t maxkey[3];              // row max keys (by part index mod 3)
     uint32_t theta[4];               // candidate threshold keys (by part index mod 4)
     PartCfg cfg[4];                  // by part index mod 4
+    uint32_t hitw[3][NDW];           // per bitmap slot and data wave: bit u set when the
+                                     // wave's float4s u hold a history position
     uint32_t lmax[2][NDW * LM_STRIDE];   // each data thread's max key of a completed part
                                          // (data wave j at j*LM_STRIDE: see LM_STRIDE)
     RowTotals tot;
@@ -183,7 +183,8 @@ __device__ __forceinline__ void issue_loads(float4 (&buf)[UP], const PipeArgs &a
 
 // Data waves: penalty (sample.c:118-128) and each thread's max key (the control wave takes
 // the part's max and candidate threshold from them); greedy rows: the wave's first argmax.
-// `mn` receives the least of the thread's logits in float4s 0..UP-2, NaN if one is NaN.
+// `mn` receives the least of the thread's logits, NaN if one is NaN (positions past the part
+// take part as the zeros their loads return, which the window test then passes).
 // The max and min propagate NaN (one v_maximum3 / v_minimum3 per pair of logits, where
 // fmaxf would first quiet each operand); a thread whose max comes out NaN takes the max of
 // its other logits, as sample.c:125-127 does (NaN never wins).  Positions past the part
@@ -195,8 +196,8 @@ __device__ __forceinline__ float min3n(float a, float b, float c) {
     return __builtin_elementwise_minimum(__builtin_elementwise_minimum(a, b), c);
 }
 __device__ __forceinline__ void complete_part(float4 (&buf)[UP], float &mn, const Geo &g,
-                                              const uint32_t *bm, const PartCfg &cf,
-                                              PipeLds &pl, int par) {
+                                              const uint32_t *bm, const uint32_t *hitw,
+                                              const PartCfg &cf, PipeLds &pl, int par) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float rp = cf.rp;
     const bool pen = (cf.flags & CFG_PEN) != 0;
@@ -209,16 +210,17 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], float &mn, cons
     float mx = -INFINITY, bv = -INFINITY;
     mn = INFINITY;
     int bi = -1;
-    uint32_t hw[UP];                                 // every history word read at once
+    // the float4s of this wavefront that hold history positions (a scalar mask), and
+    // their history words, read at once
+    const uint32_t hm = pen ? (uint32_t)__builtin_amdgcn_readfirstlane((int)hitw[wv - 1]) : 0u;
+    uint32_t hw[UP];
 #pragma unroll
-    for (int u = 0; u < UP; ++u) hw[u] = pen ? bw[u * (DT / 8)] : 0u;
+    for (int u = 0; u < UP; ++u) hw[u] = ((hm >> u) & 1u) ? bw[u * (DT / 8)] : 0u;
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
         const int c = g.c_lo + u * DT + dt;
         float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
-        if (u == UP - 1 && c >= g.c_hi)             // past the part: only the last group
-            w[0] = w[1] = w[2] = w[3] = -INFINITY;
-        if (pen) {
+        if ((hm >> u) & 1u) {                        // positions past the part are unmarked
             const uint32_t nib = __builtin_amdgcn_ubfe(hw[u], bsh, 4);
             if (__ballot(nib != 0u)) {
 #pragma unroll
@@ -226,8 +228,10 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], float &mn, cons
                     if ((nib >> k) & 1u) w[k] = penalise(w[k], rp);
             }
         }
+        mn = min3n(min3n(mn, w[0], w[1]), w[2], w[3]);
+        if (u == UP - 1 && c >= g.c_hi)             // past the part: only the last group
+            w[0] = w[1] = w[2] = w[3] = -INFINITY;
         mx = max3n(max3n(mx, w[0], w[1]), w[2], w[3]);
-        if (u < UP - 1) mn = min3n(min3n(mn, w[0], w[1]), w[2], w[3]);
         if (greedy) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
@@ -254,9 +258,10 @@ __device__ __forceinline__ void complete_part(float4 (&buf)[UP], float &mn, cons
 
 // Data waves: exact softmax numerators, partial sums, window count and candidates of one
 // part, from registers (sample.c:136-149 per element).  When the thread minima (`mn`, from
-// complete_part) of the whole wavefront are in the window, float4s 0..UP-2 skip the
-// per-logit window tests; otherwise out-of-window lanes evaluate the exp at X_OUT (inside
-// qs_expf_window's range) and their result is discarded.  A float4 holding no logit at or
+// complete_part) of the whole wavefront are in the window, its float4s skip the per-logit
+// window tests (the last one only in wavefronts without positions past the part);
+// otherwise out-of-window lanes evaluate the exp at X_OUT (inside qs_expf_window's range)
+// and their result is discarded.  A float4 holding no logit at or
 // above the threshold skips the candidate test.
 constexpr float X_OUT = -32.0f;
 
@@ -287,6 +292,9 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
     const float ths = key2f(th) * inv_t;
     const uint64_t *xtab = pl.xtab;
     const bool wave_in = __ballot(!(mn * inv_t >= thr)) == 0ull;   // NaN is not in
+    // every lane's last float4 inside the part (only the part's last wavefront has lanes
+    // past it)
+    const bool full_last = g.c_lo + (UP - 1) * DT + (wv - 1) * 64 + 63 < g.c_hi;
     // no lane whose max key (complete_part's, still in its slot) reaches th: no candidate
     // (a logit below th that the scaled test would also take is not needed: the part's
     // rejected bound is th - 1)
@@ -303,6 +311,8 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
     const int dt = data_tid();
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
+        if (u == 3) __builtin_amdgcn_s_setprio(1);   // the stage's priority steps (data_stage)
+        if (u == 4) __builtin_amdgcn_s_setprio(0);
         float sc[4];
         if (work) {
             const int c = g.c_lo + u * DT + dt;
@@ -332,7 +342,7 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
         if (!work) continue;
         uint64_t in[4];
         bool all;
-        if (u < UP - 1 && wave_in) {                // every lane's four in the window
+        if ((u < UP - 1 || full_last) && wave_in) { // every lane's four in the window
             in[0] = in[1] = in[2] = in[3] = ~0ull;
             cnt += 4 * 64;
             all = true;
@@ -453,18 +463,22 @@ __device__ __forceinline__ bool row_pen(const RowFetch &f) {
 }
 
 // Control wave: the history bitmap of this workgroup's part of a row.
-__device__ __forceinline__ void bitmap_build(uint32_t *bm, const RowFetch &f, const PipeArgs &a,
-                                             int row, const Geo &g) {
+__device__ __forceinline__ void bitmap_build(uint32_t *bm, uint32_t *hitw, const RowFetch &f,
+                                             const PipeArgs &a, int row, const Geo &g) {
     const int lane = threadIdx.x & 63;
     if (!row_pen(f)) return;
     uint4 *b4 = (uint4 *)bm;                        // bm_words is a multiple of 4
     for (int j = lane; j < g.bm_words / 4; j += 64) b4[j] = make_uint4(0u, 0u, 0u, 0u);
+    if (lane < NDW) hitw[lane] = 0u;
     const int hi = g.c_hi * 4, cap = f.param().ring_cap, head = f.head(), len = f.len();
     auto mark = [&](int p, int id) {
         int d = p - head;
         if (d < 0) d += cap;
-        if (p < cap && d < len && id >= g.lo && id < hi)
-            atomicOr(&bm[(id - g.lo) >> 5], 1u << ((id - g.lo) & 31));
+        if (p < cap && d < len && id >= g.lo && id < hi) {
+            const int q = id - g.lo, c = q >> 2, u = c / DT;   // float4 c: thread c - u*DT
+            atomicOr(&bm[q >> 5], 1u << (q & 31));
+            atomicOr(&hitw[(c - u * DT) >> 6], 1u << u);
+        }
     };
 #pragma unroll
     for (int q = 0; q < RING_PF; ++q) mark(q * 64 + lane, f.slot[q]);
@@ -736,15 +750,17 @@ __device__ __forceinline__ void data_stage(float4 (&cur)[UP], float mcur, float4
     const int p0 = s & 1;
     __syncthreads();
     // The SIMD issues for the wavefront of highest priority first (then the oldest): each
-    // data wavefront lowers its priority as it gets through the stage, so the ones behind
+    // data wavefront lowers its priority as it gets through the stage (2 for float4s 0-2
+    // of the sum, 1 for float4 3, 0 from float4 4 on, set in sum_part), so the ones behind
     // catch up and the SIMD keeps several wavefronts to switch between until the end.
     __builtin_amdgcn_s_setprio(2);
     const PartLoad nl(a, r3, v3, g);              // part s+3, into `cur` as it is summed
     sum_part(cur, mcur, nl, v0, g, pl.cfg[s & 3], ckey + p0 * PCAP, cid + p0 * PCAP,
              pl.maxkey[s % 3], pl.theta[s & 3], pl, p0);
-    __builtin_amdgcn_s_setprio(1);
-    if (v2) complete_part(ld, mld, g, bm + ((s + 2) % 3) * g.bm_words, pl.cfg[(s + 2) & 3], pl, p0);
     __builtin_amdgcn_s_setprio(0);
+    if (v2)
+        complete_part(ld, mld, g, bm + ((s + 2) % 3) * g.bm_words, pl.hitw[(s + 2) % 3],
+                      pl.cfg[(s + 2) & 3], pl, p0);
 }
 
 // One stage, control wave: publish part s+1's max (completed during the previous stage),
@@ -777,7 +793,7 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
         if (lane == 0) pl.theta[(s + 1) & 3] = th;
     }
     if (v3) {
-        bitmap_build(bm + (s % 3) * g.bm_words, f3, a, r3, g);   // part s+3's slot
+        bitmap_build(bm + (s % 3) * g.bm_words, pl.hitw[s % 3], f3, a, r3, g);   // s+3's slot
         set_cfg(pl.cfg[(s + 3) & 3], f3.param(), row_pen(f3));   // part s-1's settings are used
     }
     if (rel) control_release(a, rs);
@@ -819,10 +835,10 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         issue_loads(B1, a, r1, t1, g);
         for (int j = tid - 64; j < QS_EXPF_XTAB_N; j += DT) pl.xtab[j] = qs_expf_xtab_entry(pl.dl.tab, j);
         __syncthreads();                         // part 0's bitmap and settings
-        if (t0) complete_part(B0, M0, g, bm, pl.cfg[0], pl, 0);
+        if (t0) complete_part(B0, M0, g, bm, pl.hitw[0], pl.cfg[0], pl, 0);
         __syncthreads();                         // part 0's max is exchanged meanwhile
         issue_loads(B2, a, r2, t2, g);
-        if (t1) complete_part(B1, M1, g, bm + g.bm_words, pl.cfg[1], pl, 1);   // slot 1
+        if (t1) complete_part(B1, M1, g, bm + g.bm_words, pl.hitw[1], pl.cfg[1], pl, 1);
         // buffer roles rotate with period 3; whole rotations only (stages past the last
         // one do nothing), so every pass through the loop leaves the same loads in flight
         // (the next part's, in B2) and each wait covers only the loads it needs
@@ -845,16 +861,16 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         if (tid < QS_EXPF_TAB_N) pl.dl.tab[tid] = c_exp_tab_p[tid];   // after the fetches
         __syncthreads();
         if (t0) {
-            bitmap_build(bm, f0, a, r0, g);
+            bitmap_build(bm, pl.hitw[0], f0, a, r0, g);
             set_cfg(pl.cfg[0], f0.param(), row_pen(f0));
         }
         __syncthreads();                             // part 0 is completed meanwhile
         if (t1) {
-            bitmap_build(bm + g.bm_words, f1, a, r1, g);
+            bitmap_build(bm + g.bm_words, pl.hitw[1], f1, a, r1, g);
             set_cfg(pl.cfg[1], f1.param(), row_pen(f1));
         }
         if (t2) {                                    // used from stage 0 on
-            bitmap_build(bm + 2 * g.bm_words, f2, a, r2, g);
+            bitmap_build(bm + 2 * g.bm_words, pl.hitw[2], f2, a, r2, g);
             set_cfg(pl.cfg[2], f2.param(), row_pen(f2));
         }
         __syncthreads();
@@ -873,9 +889,9 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     }
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
-    {                                // the last summed part, unless the loop stored it
+    if (!data) {                     // the last summed part, unless the loop stored it
         const int s = a.stages_pad - 1;
-        if (!data && s >= 0 && task_valid(a, s, g, w))
+        if (s >= 0 && task_valid(a, s, g, w))
             if (control_store(a, task_row(s, w, g.rps), g, pl.maxkey[s % 3], pl.theta[s & 3],
                               ckey + (s & 1) * PCAP, cid + (s & 1) * PCAP, pl.cfg[s & 3], pl,
                               s & 1))
