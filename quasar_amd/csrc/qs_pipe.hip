@@ -390,22 +390,27 @@ __device__ __forceinline__ void sum_part(float4 (&buf)[UP], float mn, const Part
 }
 
 // Control wave: wait (bounded) until all parts of `row` published their max key (one slot
-// per part, 0 until published: keys of part maxima are never 0); the row max key.
-__device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row) {
+// per part, 0 until published: keys of part maxima are never 0); the row max key.  `k`
+// holds lane i's first read of part i's slot (rowmax_slots), taken ahead by the caller so
+// that its latency passes during other work.
+__device__ __forceinline__ uint32_t poll_rowmax(const PipeArgs &a, int row, uint32_t k) {
     const int lane = threadIdx.x & 63;
     const uint32_t *slot = a.sc.rowmax + (int64_t)row * PARTS;
-    uint32_t k = 0u;
     int it = 0;
-    while (true) {
-        k = lane < PARTS ? ld_dev(&slot[lane]) : 1u;
-        if (__ballot(k == 0u) == 0ull) break;
+    while (__ballot(k == 0u) != 0ull) {
         if (++it >= SPIN_LIMIT) {
             if (lane == 0) atomicOr(a.sc.err, 2);
             break;
         }
         __builtin_amdgcn_s_sleep(1);
+        k = lane < PARTS ? ld_dev(&slot[lane]) : 1u;
     }
     return wave_max_u(lane < PARTS ? k : 0u);
+}
+// The first read of those slots (lane i: part i's), issued ahead of the poll.
+__device__ __forceinline__ uint32_t rowmax_slots(const PipeArgs &a, int row) {
+    const int lane = threadIdx.x & 63;
+    return lane < PARTS ? ld_dev(&a.sc.rowmax[(int64_t)row * PARTS + lane]) : 1u;
 }
 
 // Control wave: a row's parameters, history ring position and the first RING_PF*64 ring
@@ -788,7 +793,11 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
     if (sv)
         rel = control_store(a, rs, g, pl.maxkey[(s + 2) % 3], pl.theta[(s + 3) & 3],
                             ckey + p1 * PCAP, cid + p1 * PCAP, pl.cfg[(s + 3) & 3], pl, p1);
-    if (v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY)) {
+    // the row max: the partners' slots read now (after the stores, which the wait for this
+    // read then covers), looked at after the threshold and bitmap
+    const bool sampled = v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY);
+    const uint32_t k0 = sampled ? rowmax_slots(a, r1) : 1u;
+    if (sampled) {
         const uint32_t th = part_theta(tp, pl.lmax[p1], pl.cfg[(s + 1) & 3]);
         if (lane == 0) pl.theta[(s + 1) & 3] = th;
     }
@@ -796,11 +805,11 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
         bitmap_build(bm + (s % 3) * g.bm_words, pl.hitw[s % 3], f3, a, r3, g);   // s+3's slot
         set_cfg(pl.cfg[(s + 3) & 3], f3.param(), row_pen(f3));   // part s-1's settings are used
     }
-    if (rel) control_release(a, rs);
-    if (v1 && !(pl.cfg[(s + 1) & 3].flags & CFG_GREEDY)) {
-        const uint32_t key = poll_rowmax(a, r1);
+    if (sampled) {
+        const uint32_t key = poll_rowmax(a, r1, k0);
         if (lane == 0) pl.maxkey[(s + 1) % 3] = key;
     }
+    if (rel) control_release(a, rs);              // the stores completed before the poll
 }
 
 __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
@@ -881,7 +890,7 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
             if ((tid & 63) == 0) pl.theta[0] = th;
         }
         if (t0 && !(pl.cfg[0].flags & CFG_GREEDY)) {
-            const uint32_t key = poll_rowmax(a, r0);
+            const uint32_t key = poll_rowmax(a, r0, rowmax_slots(a, r0));
             if ((tid & 63) == 0) pl.maxkey[0] = key;
         }
 
