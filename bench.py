@@ -24,6 +24,8 @@ Also reported on the same JSON line:
   parity        the first step's ids against the CPU on every sampled row
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--mode M]
        python bench.py --calibrate-copy [--copy-mib N]   (copies of N MiB, for the counters)
+       python bench.py --router [--router-tokens T]      (the MoE router's expert choice:
+                                                           T tokens x 128 experts, top 8)
 """
 import argparse
 import json
@@ -59,6 +61,9 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run plain device copies of --copy-mib MiB (counter calibration)")
     ap.add_argument("--copy-mib", type=int, default=512)
+    ap.add_argument("--router", action="store_true",
+                    help="only time qs_router_topk (128 experts, 8 used, renormalised)")
+    ap.add_argument("--router-tokens", type=int, default=4096)
     return ap.parse_args()
 
 
@@ -119,6 +124,43 @@ def cpu_baseline(w, logits_host, hist, seeds, gpu_ids, args):
                       f"{threads} POSIX threads, one sampler per row"}, mism, B
 
 
+def router_bench(args):
+    """The mixture-of-experts router's choice (qs_router_topk) on `--router-tokens`
+    tokens of 128 router logits, 8 experts used, weights renormalised (a 128-expert,
+    top-8 model's router per layer): tokens/s over back-to-back calls between HIP events,
+    the output checked against the CPU restatement, which is also timed."""
+    import quasar_amd as qa
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from pyoracle import Oracle
+    T, E, U = args.router_tokens, 128, 8
+    x = (np.random.default_rng(7).standard_normal((T, E)) * 3.0).astype(np.float32)
+    buf = qa.DeviceBuffer.from_array(x)
+    di, dw = qa.DeviceBuffer(4 * T * U), qa.DeviceBuffer(4 * T * U)
+    qa.router_topk(buf, T, E, U, 1, di, dw)
+    orc = Oracle()
+    t0 = time.perf_counter()
+    oi, ow = orc.router_topk(x, U, 1)
+    cpu_s = time.perf_counter() - t0
+    gi = di.download(np.int32, T * U).reshape(T, U)
+    gw = dw.download(np.float32, T * U).reshape(T, U)
+    mism = int(((gi != oi).any(axis=1) | (gw.view(np.uint32) != ow.view(np.uint32)).any(axis=1)).sum())
+    qa.router_time(buf, T, E, U, 1, di, dw, args.warmup)
+    ms = qa.router_time(buf, T, E, U, 1, di, dw, args.steps)
+    us = ms * 1e3 / args.steps
+    print(json.dumps({
+        "metric": "MoE router choices/s (128 experts, top 8, renormalised)",
+        "value": T / (us * 1e-6), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": us / 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "moe_router", "tokens": T, "experts": E, "used": U,
+                   "norm_topk": True},
+        "cpu_baseline": {"value": T / cpu_s, "unit": "tokens/s", "cores": 1, "kind": "port",
+                         "sample": f"all {T} tokens once through the CPU restatement"},
+        "parity": {"tokens_checked": T, "mismatches": mism}}), flush=True)
+    for b_ in (buf, di, dw):
+        b_.free()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -128,6 +170,8 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         return calibrate_copy(args)
+    if args.router:
+        return router_bench(args)
     import quasar_amd as qa
     from quasar_amd.workloads import BENCH_WORKLOAD, STRESS, WORKLOADS
     sys.path.insert(0, os.path.join(ROOT, "oracle"))

@@ -11,6 +11,9 @@
  * Part 3 is plumbing for callers without their own GPU runtime (tests, the benchmark):
  * device buffers, copies, the synthetic-input generator and event timing.
  *
+ * Part 4 is the mixture-of-experts router's expert choice, the same selection at 128
+ * experts per token (the reference's forward_cpu.c:296-304).
+ *
  * Return codes of the extension functions: 0 on success, QS_EINVAL for bad arguments,
  * QS_ENOMEM when device memory cannot be allocated, QS_EDEVICE for any other HIP
  * failure; qs_last_error() describes the last failure on the calling thread.
@@ -191,6 +194,35 @@ int qs_expf_device(const float *d_x, float *d_y, int64_t n);
 int qs_batch_time_picks(qs_batch *b, const float *const *d_logits, int n_buffers,
                         int64_t row_stride, int n_rows, int n_vocab, int32_t *d_out, int iters,
                         float *ms);
+
+/* ------------------------------------------------------------------------------------
+ * Part 4: the mixture-of-experts router's expert choice (extension)
+ *
+ * Replaces forward_cpu.c:296-304 (softmax of the router logits, forward_cpu.c:165-172,
+ * then n_used strict-`>` arg-max scans, then the optional renormalisation), for a batch
+ * of tokens whose router logits are on the device.  No counterpart in sample.h: the
+ * reference runs it inline in its CPU forward pass.
+ * ------------------------------------------------------------------------------------ */
+
+/* For each token t < n_tokens, from d_logits[t*row_stride + e], e < n_expert: the
+ * softmax p (libm-equal expf, the reference's sequential float sum), then the n_used
+ * experts of largest p (lowest index among equal p; never a NaN) into
+ * d_idx[t*n_used + s] and their p into d_wt[t*n_used + s], slot s in choice order; with
+ * norm_topk != 0 the weights are divided by their sequential sum when it is positive.
+ * Bit-identical to the reference.  A slot left with nothing to take (every remaining p
+ * NaN, where the reference reads index -1) gets expert -1 and weight 0.
+ * 1 <= n_expert <= 256, 1 <= n_used <= min(64, n_expert), row_stride >= n_expert (the
+ * reference's array bounds).  Asynchronous on `stream` (a hipStream_t; NULL for the
+ * default stream). */
+int qs_router_topk(const float *d_logits, int64_t row_stride, int n_tokens, int n_expert,
+                   int n_used, int norm_topk, int32_t *d_idx, float *d_wt, void *stream);
+
+/* Enqueue `iters` back-to-back qs_router_topk calls between two HIP events on a stream of
+ * its own, wait, and return the elapsed milliseconds in *ms (plumbing for the
+ * benchmark). */
+int qs_router_time(const float *d_logits, int64_t row_stride, int n_tokens, int n_expert,
+                   int n_used, int norm_topk, int32_t *d_idx, float *d_wt, int iters,
+                   float *ms);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,7 @@
  *   orc_xorshift64, orc_rng_unit              sample.c:72-77, 79-81
  *   orc_record                                sample.c:83-92
  *   orc_pick_row                              sample.c:111-179
+ *   orc_router_topk (orc_router.c)            forward_cpu.c:165-172, 296-304
  * using the host C library's expf (sample.c:148) and an explicit (p desc, id asc) order
  * for the sort (sample.c:106-109,151: glibc's qsort is a stable merge sort on an
  * ascending-id array, so equal p keep ascending ids).
@@ -93,6 +94,11 @@ void  orc_libm_expf_array(const float *x, float *y, long n);
 /* Count x in [lo, hi] (by float ordering, both finite) where the product expf differs
  * from the host expf; n_threads POSIX threads. */
 long  orc_check_expf_range(float lo, float hi, int n_threads);
+
+/* forward_cpu.c:165-172, 296-304: the mixture-of-experts router's choice per token
+ * (orc_router.c): idx/wt hold n_used slots per token. */
+void orc_router_topk(const float *logits, long row_stride, int n_tokens, int n_expert,
+                     int n_used, int norm_topk, int32_t *idx, float *wt);
 
 #ifdef __cplusplus
 }

@@ -183,6 +183,19 @@ class Oracle:
         lib.orc_libm_expf_array.argtypes = [_F, _F, C.c_long]
         lib.orc_check_expf_range.argtypes = [C.c_float, C.c_float, C.c_int]
         lib.orc_check_expf_range.restype = C.c_long
+        lib.orc_router_topk.argtypes = [_F, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int, _I,
+                                        _F]
+
+    def router_topk(self, logits, n_used, norm_topk):
+        """forward_cpu.c:165-172, 296-304 on each row of `logits` (tokens x experts):
+        (idx, wt), each tokens x n_used."""
+        a = np.ascontiguousarray(logits, dtype=np.float32)
+        t, e = a.shape
+        idx = np.zeros((t, n_used), dtype=np.int32)
+        wt = np.zeros((t, n_used), dtype=np.float32)
+        self.lib.orc_router_topk(_fptr(a), e, t, e, n_used, 1 if norm_topk else 0, _iptr(idx),
+                                 _fptr(wt))
+        return idx, wt
 
     def sampler(self):
         s = _SamplerBase(self.lib, "orc_sampler_", "orc_sampler_")

@@ -70,6 +70,25 @@ def gen_logits_device(buf, row_stride, row0, n_rows, n_vocab, dist, sigma, boost
           "qs_gen_logits_device")
 
 
+def router_topk(logits, n_tokens, n_expert, n_used, norm_topk, idx, wt, row_stride=None):
+    """The mixture-of-experts router's choice (qs_router_topk) for n_tokens rows of router
+    logits in DeviceBuffer `logits`; slots into DeviceBuffers `idx` (int32) and `wt`
+    (float32), n_used per token.  Waits for the device."""
+    lib = load()
+    check(lib.qs_router_topk(logits.ptr, row_stride or n_expert, n_tokens, n_expert, n_used,
+                             1 if norm_topk else 0, idx.ptr, wt.ptr, None), "qs_router_topk")
+    check(lib.qs_device_synchronize(), "qs_device_synchronize")
+
+
+def router_time(logits, n_tokens, n_expert, n_used, norm_topk, idx, wt, iters):
+    """Milliseconds for `iters` back-to-back router_topk calls (qs_router_time)."""
+    ms = C.c_float()
+    check(load().qs_router_time(logits.ptr, n_expert, n_tokens, n_expert, n_used,
+                                1 if norm_topk else 0, idx.ptr, wt.ptr, iters, C.byref(ms)),
+          "qs_router_time")
+    return ms.value
+
+
 def copy_device(dst, src, nbytes, iters=1):
     """`iters` plain streaming copies of nbytes from src to dst (DeviceBuffers): a kernel of
     known memory traffic for calibrating hardware counters."""
