@@ -66,9 +66,9 @@ k_router(const float *logits, int64_t stride, int n_tokens, int n_expert, int n_
     if (threadIdx.x < QS_EXPF_TAB_N) tab[threadIdx.x] = c_exp_tab_r[threadIdx.x];
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * RT_WAVES + (threadIdx.x >> 6);
+    const int64_t t = (int64_t)blockIdx.x * RT_WAVES + (threadIdx.x >> 6);
     if (t >= n_tokens) return;                       // whole wavefronts
-    const float *a = logits + (int64_t)t * stride;
+    const float *a = logits + t * stride;
 
     // forward_cpu.c:166-167: mx = a[0], then every later a[i] > mx replaces it: a NaN
     // a[0] stays, later NaNs never enter.  fmaxf drops NaNs the same way.
@@ -129,8 +129,8 @@ k_router(const float *logits, int64_t stride, int n_tokens, int n_expert, int n_
         if (sm > 0.0f) wt_mine = wt_mine / sm;
     }
     if (lane < n_used) {
-        out_idx[(int64_t)t * n_used + lane] = idx_mine;
-        out_wt[(int64_t)t * n_used + lane] = wt_mine;
+        out_idx[t * n_used + lane] = idx_mine;
+        out_wt[t * n_used + lane] = wt_mine;
     }
 }
 
@@ -147,7 +147,7 @@ int qs_router_topk(const float *d_logits, int64_t row_stride, int n_tokens, int 
         return QS_EINVAL;
     }
     if (n_tokens == 0) return 0;
-    const unsigned blocks = (unsigned)((n_tokens + RT_WAVES - 1) / RT_WAVES);
+    const unsigned blocks = (unsigned)(((int64_t)n_tokens + RT_WAVES - 1) / RT_WAVES);
     hipLaunchKernelGGL(k_router, dim3(blocks), dim3(64 * RT_WAVES), 0, (hipStream_t)stream,
                        d_logits, row_stride, n_tokens, n_expert, n_used, norm_topk ? 1 : 0,
                        d_idx, d_wt);
