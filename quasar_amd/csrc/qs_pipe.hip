@@ -69,8 +69,6 @@ struct PipeArgs {
     int n_rows;
     int part_len;                    // elements per part (multiple of 4)
     int stages;
-    int stages_pad;                  // stages rounded up to a multiple of 3: the stage loops
-                                     // run whole rotations of the three register buffers
     RowState st;
     Scratch sc;
     int32_t *out;
@@ -848,12 +846,14 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
         __syncthreads();                         // part 0's max is exchanged meanwhile
         issue_loads(B2, a, r2, t2, g);
         if (t1) complete_part(B1, M1, g, bm + g.bm_words, pl.hitw[1], pl.cfg[1], pl, 1);
-        // buffer roles rotate with period 3; whole rotations only (stages past the last
-        // one do nothing), so every pass through the loop leaves the same loads in flight
-        // (the next part's, in B2) and each wait covers only the loads it needs
-        for (int s = 0; s < a.stages_pad; s += 3) {
+        // buffer roles rotate with period 3: every full pass through the loop leaves the
+        // same loads in flight (the next part's, in B2) and each wait covers only the
+        // loads it needs; the last pass stops after the last stage
+        for (int s = 0; s < a.stages; s += 3) {
             data_stage(B0, M0, B2, M2, s, a, g, w, bm, ckey, cid, pl);
+            if (s + 1 >= a.stages) break;
             data_stage(B1, M1, B0, M0, s + 1, a, g, w, bm, ckey, cid, pl);
+            if (s + 2 >= a.stages) break;
             data_stage(B2, M2, B1, M1, s + 2, a, g, w, bm, ckey, cid, pl);
         }
     } else {
@@ -894,12 +894,12 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
             if ((tid & 63) == 0) pl.maxkey[0] = key;
         }
 
-        for (int s = 0; s < a.stages_pad; ++s) control_stage(s, rp, a, g, w, bm, ckey, cid, pl);
+        for (int s = 0; s < a.stages; ++s) control_stage(s, rp, a, g, w, bm, ckey, cid, pl);
     }
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     if (!data) {                     // the last summed part, unless the loop stored it
-        const int s = a.stages_pad - 1;
+        const int s = a.stages - 1;
         if (s >= 0 && task_valid(a, s, g, w))
             if (control_store(a, task_row(s, w, g.rps), g, pl.maxkey[s % 3], pl.theta[s & 3],
                               ckey + (s & 1) * PCAP, cid + (s & 1) * PCAP, pl.cfg[s & 3], pl,
@@ -962,7 +962,6 @@ int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vo
     a.part_len = ((n_vocab + PARTS - 1) / PARTS + 3) / 4 * 4;
     const int rps = grid / PARTS;
     a.stages = (n_rows + rps - 1) / rps;
-    a.stages_pad = (a.stages + 2) / 3 * 3;
     a.st = st;
     a.sc = sc;
     a.out = out;
