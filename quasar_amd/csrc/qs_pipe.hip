@@ -540,10 +540,45 @@ __device__ __forceinline__ Top3 quad_top3(const uint32_t *lm) {
     return Top3{t1, t2, t3};
 }
 
+// The four largest thread max keys of each data wave, as quad_top3 (lanes 4j..4j+3 hold
+// data wave j's); for parts whose kw exceeds what the top three give.
+struct Top4 {
+    uint32_t t1, t2, t3, t4;
+};
+__device__ __forceinline__ void top4_insert(Top4 &t, uint32_t v) {
+    const uint32_t n1 = max(t.t1, v), n2 = umed3(t.t1, t.t2, v), n3 = umed3(t.t2, t.t3, v),
+                   n4 = umed3(t.t3, t.t4, v);
+    t = Top4{n1, n2, n3, n4};
+}
+__device__ __forceinline__ Top4 quad_top4(const uint32_t *lm) {
+    const int lane = threadIdx.x & 63, j = lane >> 2;
+    Top4 t{0u, 0u, 0u, 0u};                          // thread max keys are never 0
+    if (j < NDW) {
+        const uint32_t *src = lm + j * LM_STRIDE + (lane & 3) * 16;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) top4_insert(t, src[i]);
+    }
+    {
+        const Top4 o{xor_lane<1>(t.t1), xor_lane<1>(t.t2), xor_lane<1>(t.t3), xor_lane<1>(t.t4)};
+        top4_insert(t, o.t1);
+        top4_insert(t, o.t2);
+        top4_insert(t, o.t3);
+        top4_insert(t, o.t4);
+    }
+    {
+        const Top4 o{xor_lane<2>(t.t1), xor_lane<2>(t.t2), xor_lane<2>(t.t3), xor_lane<2>(t.t4)};
+        top4_insert(t, o.t1);
+        top4_insert(t, o.t2);
+        top4_insert(t, o.t3);
+        top4_insert(t, o.t4);
+    }
+    return t;
+}
+
 // Control wave: the part's candidate threshold, the kw-th largest of a set of thread max
 // keys (kw distinct logits of the part reach it; the part keeps every logit at or above
 // it, and every other one lies below it).  The set is each data wave's three largest
-// (from quad_top3) or, when kw exceeds those, all of them.
+// (from quad_top3), or four largest (quad_top4) when kw exceeds those, or all of them.
 __device__ __forceinline__ uint32_t part_theta(const Top3 &tp, const uint32_t *lm,
                                                const PartCfg &cf) {
     const int lane = threadIdx.x & 63;
@@ -552,6 +587,14 @@ __device__ __forceinline__ uint32_t part_theta(const Top3 &tp, const uint32_t *l
         // the 45 values one per lane (lane 4j+q: wave j's (q+1)-th), sorted: the kw-th
         const int q = lane & 3;
         uint32_t v = ((lane >> 2) < NDW && q < 3) ? (q == 0 ? tp.t1 : q == 1 ? tp.t2 : tp.t3) : 0u;
+        v = wave_sort_desc_u32(v);
+        th = (uint32_t)__builtin_amdgcn_readlane((int)v, cf.kw - 1);
+    } else if (cf.kw <= 4 * NDW) {
+        // the 60 values one per lane (lane 4j+q: wave j's (q+1)-th), sorted: the kw-th
+        const Top4 t4 = quad_top4(lm);
+        const int q = lane & 3;
+        uint32_t v = (lane >> 2) < NDW ? (q == 0 ? t4.t1 : q == 1 ? t4.t2 : q == 2 ? t4.t3 : t4.t4)
+                                       : 0u;
         v = wave_sort_desc_u32(v);
         th = (uint32_t)__builtin_amdgcn_readlane((int)v, cf.kw - 1);
     } else {
