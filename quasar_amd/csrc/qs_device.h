@@ -521,6 +521,61 @@ __device__ __forceinline__ void bitonic_desc(uint64_t *s, int n_pad) {
     }
 }
 
+// The same sort by one wavefront over 64*Q keys held Q per lane (element q*64 + lane in
+// v[q]): strides below 64 exchange lanes, larger ones exchange registers of a lane.  The
+// compare-exchange network is bitonic_desc's, so the order is the same; no barrier.
+template <int Q, int SIZE, int S>
+__device__ __forceinline__ void bitonic_step_q(uint64_t (&v)[Q], int lane) {
+    if constexpr (S >= 64) {
+        constexpr int R = S / 64;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            if ((q & R) == 0) {
+                const bool desc = ((q * 64) & SIZE) == 0;
+                const uint64_t a = v[q], b = v[q | R];
+                const bool sw = (a < b) == desc;
+                v[q] = sw ? b : a;
+                v[q | R] = sw ? a : b;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const uint64_t o = xor_lane64<S>(v[q]);
+            const bool desc = SIZE >= 64 ? (((q * 64) & SIZE) == 0) : ((lane & SIZE) == 0);
+            const bool keep_max = ((lane & S) == 0) == desc;
+            v[q] = keep_max ? (o > v[q] ? o : v[q]) : (o < v[q] ? o : v[q]);
+        }
+    }
+}
+template <int Q, int SIZE, int S>
+__device__ __forceinline__ void bitonic_strides_q(uint64_t (&v)[Q], int lane) {
+    if constexpr (S >= 1) {
+        bitonic_step_q<Q, SIZE, S>(v, lane);
+        bitonic_strides_q<Q, SIZE, S / 2>(v, lane);
+    }
+}
+template <int Q, int SIZE>
+__device__ __forceinline__ void bitonic_sizes_q(uint64_t (&v)[Q], int lane) {
+    if constexpr (SIZE <= 64 * Q) {
+        bitonic_strides_q<Q, SIZE, SIZE / 2>(v, lane);
+        bitonic_sizes_q<Q, SIZE * 2>(v, lane);
+    }
+}
+// Sort s[0, n) descending in place, n <= 64*Q, by the calling wavefront; slots from n on
+// enter as 0 (below every key) and are neither read nor written.
+template <int Q>
+__device__ __forceinline__ void wave_sort_lds_desc(uint64_t *s, int n) {
+    const int lane = threadIdx.x & 63;
+    uint64_t v[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) v[q] = q * 64 + lane < n ? s[q * 64 + lane] : 0ull;
+    bitonic_sizes_q<Q, 2>(v, lane);
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+        if (q * 64 + lane < n) s[q * 64 + lane] = v[q];
+}
+
 // (p, id) sort key: p's bits above, ~id below, so descending order is p desc, id asc
 // (sample.c:151 under glibc's stable merge sort on ascending ids).
 __device__ __forceinline__ uint64_t pid_key(float p, int id) {
@@ -586,11 +641,72 @@ __device__ __forceinline__ bool decide_prefix_f(PF &&pf, IF &&idf, int E, int nw
     return true;
 }
 
+// f(i, p) over the probabilities of s[lo, hi) in order until it returns true; returns
+// that i, or hi.  Eight keys are read ahead of their turn (indexes clamped to hi - 1), so
+// one thread's ordered sums wait on the LDS once per eight positions.
+template <typename F>
+__device__ __forceinline__ int scan_p(const uint64_t *s, int lo, int hi, F &&f) {
+    for (int i0 = lo; i0 < hi; i0 += 8) {
+        float p[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) p[k] = key_p(s[min(i0 + k, hi - 1)]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (i0 + k < hi && f(i0 + k, p[k])) return i0 + k;
+    }
+    return hi;
+}
+
+// decide_prefix_f over sorted keys in LDS, one thread: the same cuts, sums (in the same
+// order) and results, each loop a scan_p.
 __device__ __forceinline__ bool decide_prefix(const uint64_t *srt, int E, int nwin,
                                               const qs_row_param &P, uint64_t &rs, int &id,
                                               qs_pick_diag &d) {
-    return decide_prefix_f([&](int i) { return key_p(srt[i]); },
-                           [&](int i) { return key_id(srt[i]); }, E, nwin, P, rs, id, d);
+    if (E < 1) return false;
+    int n = nwin;                                             // sample.c:153-154
+    if (P.top_k > 0 && P.top_k < n) n = P.top_k;
+    d.keep_topk = n;
+    if (P.top_p < 1.0f) {                                     // sample.c:155-160
+        double cum = 0.0;
+        const int lim = min(n, E);
+        const int j = scan_p(srt, 0, lim, [&](int, float p) {
+            cum += p;
+            return cum >= P.top_p;
+        });
+        if (j < lim) n = j + 1;
+        else if (n > E) return false;                         // the cut reads past E
+    }
+    d.keep_topp = n;
+    const float p0 = key_p(srt[0]);
+    if (P.min_p > 0.0f) {                                     // sample.c:161-168
+        const float floor_p = P.min_p * p0;
+        const int lim = min(n, E);
+        const int j = scan_p(srt, 1, lim, [&](int, float p) { return p < floor_p; });
+        if (j < lim) n = j;
+        else if (n > E) return false;
+    }
+    if (n < 1) n = 1;
+    if (n > E) return false;
+    double rsum = 0.0;                                        // sample.c:170-175
+    scan_p(srt, 0, n, [&](int, float p) {
+        rsum += p;
+        return false;
+    });
+    const double u = rng_unit(rs);
+    const double r = u * rsum;
+    double acc = 0.0;
+    const int j = scan_p(srt, 0, n, [&](int, float p) {
+        acc += p;
+        return r <= acc;
+    });
+    const int rank = j < n ? j : n - 1;
+    id = key_id(srt[rank]);
+    d.keep = n;
+    d.rank = rank;
+    d.rsum = rsum;
+    d.u = u;
+    d.p0 = p0;
+    return true;
 }
 
 // decide_prefix_f for a wavefront whose lane i holds the (p, id) key of position i (lanes
@@ -972,22 +1088,39 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
         while (npad < nkept) npad <<= 1;
         for (int j = nkept + tid; j < npad; j += NT) srt[j] = 0ull;
         __syncthreads();
-        bitonic_desc<NT>(srt, npad);
-        if (tid == 0) {
-            const float inv = (float)(1.0 / t.sum);
-            int m = 0;                         // in-window candidates (p > 0) sort first
-            while (m < nkept && (srt[m] >> 32) != 0ull) ++m;
-            // The largest probability any rejected logit can have (p is monotone in it).
-            float p_rej = -1.0f;
-            if (rej > KEY_NEG_INF) {
-                const float s = key2f(rej) * inv_t;
-                if (s >= thr) p_rej = qs_expf_core(s - msc, tab) * inv;
+        if (npad <= 512) {                          // one wavefront, no barriers
+            if (tid < 64) {
+                if (npad <= 64) wave_sort_lds_desc<1>(srt, npad);
+                else if (npad <= 128) wave_sort_lds_desc<2>(srt, npad);
+                else if (npad <= 256) wave_sort_lds_desc<4>(srt, npad);
+                else wave_sort_lds_desc<8>(srt, npad);
             }
-            // Positions [0, E) of the sorted candidates are positions of the full order.
-            int E = m;
-            if (m < t.nwin)
-                for (int i = 0; i < m; ++i)
-                    if (key_p(srt[i]) <= p_rej) { E = i; break; }
+            __syncthreads();
+        } else {
+            bitonic_desc<NT>(srt, npad);
+        }
+        const float inv = (float)(1.0 / t.sum);
+        // in-window candidates (p > 0) sort first: m is the first position with p = 0
+        if (tid == 0) { dl.sh[1] = nkept; dl.sh[2] = nkept; }
+        __syncthreads();
+        for (int j = tid; j < nkept; j += NT)
+            if ((srt[j] >> 32) == 0ull) atomicMin(&dl.sh[1], j);
+        __syncthreads();
+        const int m = dl.sh[1];
+        // The largest probability any rejected logit can have (p is monotone in it).
+        float p_rej = -1.0f;
+        if (rej > KEY_NEG_INF) {
+            const float s = key2f(rej) * inv_t;
+            if (s >= thr) p_rej = qs_expf_core(s - msc, tab) * inv;
+        }
+        // Positions [0, E) of the sorted candidates are positions of the full order: E is
+        // the first position whose p is at most p_rej (when the window is not all here).
+        if (m < t.nwin)
+            for (int j = tid; j < m; j += NT)
+                if (key_p(srt[j]) <= p_rej) atomicMin(&dl.sh[2], j);
+        __syncthreads();
+        const int E = min(m, dl.sh[2]);
+        if (tid == 0) {
             qs_pick_diag d;
             memset(&d, 0, sizeof d);
             uint64_t rs = st.rng[row];
