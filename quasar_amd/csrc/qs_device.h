@@ -1006,6 +1006,89 @@ struct DecideLds {
     uint32_t shu[2];
 };
 
+// decide_prefix by one wavefront over positions [0, 64*Q) of sorted keys in LDS, from
+// inclusive prefix sums in double instead of running sums.  They are the same numbers
+// when every probability read is 0 or in [2^-29, 2) and their total is below 2: every
+// such float is a multiple of 2^-52, so every partial sum is a multiple of 2^-52 below 2
+// and exact in double, whatever the order of the additions.  Returns 1 when decided (rs,
+// id and d as decide_prefix gives them), 0 where decide_prefix returns false, -1 (nothing
+// consumed) when the sums might not be exact or the positions do not fit: the caller
+// then runs decide_prefix.  Every lane of the wavefront gets the same results.
+template <int Q>
+__device__ __forceinline__ int decide_prefix_par(const uint64_t *srt, int E, int nwin,
+                                                 const qs_row_param &P, uint64_t &rs, int &id,
+                                                 qs_pick_diag &d) {
+    const int lane = threadIdx.x & 63;
+    if (E < 1) return 0;
+    int n = nwin;                                             // sample.c:153-154
+    if (P.top_k > 0 && P.top_k < n) n = P.top_k;
+    const int lim = min(n, E);          // the loops of decide_prefix read positions < lim
+    if (lim < 1 || lim > 64 * Q) return -1;
+    float p[Q];
+    double c[Q];
+    double carry = 0.0;
+    bool bad = false;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int i = q * 64 + lane;
+        p[q] = i < lim ? key_p(srt[i]) : 0.0f;
+        const uint32_t b = __float_as_uint(p[q]);
+        bad |= (b != 0u && b < 0x31000000u) || b >= 0x40000000u;   // not 0 or [2^-29, 2)
+        double x = (double)p[q];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const double y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        c[q] = x + carry;
+        carry = __shfl(c[q], 63, 64);
+    }
+    if (__ballot(bad) != 0ull || !(carry < 2.0)) return -1;
+    // the first position below `end` (and from `beg`) where pred holds, or `end`
+    auto first = [&](int beg, int end, auto &&pred) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int i = q * 64 + lane;
+            const uint64_t m = __ballot(i >= beg && i < end && pred(q));
+            if (m) return q * 64 + (int)__builtin_ctzll(m);
+        }
+        return end;
+    };
+    d.keep_topk = n;
+    if (P.top_p < 1.0f) {                                     // sample.c:155-160
+        const int j = first(0, lim, [&](int q) { return c[q] >= P.top_p; });
+        if (j < lim) n = j + 1;
+        else if (n > E) return 0;
+    }
+    d.keep_topp = n;
+    const float p0 = __shfl(p[0], 0, 64);
+    if (P.min_p > 0.0f) {                                     // sample.c:161-168
+        const float floor_p = P.min_p * p0;
+        const int lim2 = min(n, E);
+        const int j = first(1, lim2, [&](int q) { return p[q] < floor_p; });
+        if (j < lim2) n = j;
+        else if (n > E) return 0;
+    }
+    if (n < 1) n = 1;
+    if (n > E) return 0;
+    double cl = 0.0;                                          // sample.c:170-175
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+        if (q == ((n - 1) >> 6)) cl = c[q];
+    const double rsum = __shfl(cl, (n - 1) & 63, 64);
+    const double u = rng_unit(rs);
+    const double r = u * rsum;
+    const int j = first(0, n, [&](int q) { return r <= c[q]; });
+    const int rank = j < n ? j : n - 1;
+    id = key_id(srt[rank]);
+    d.keep = n;
+    d.rank = rank;
+    d.rsum = rsum;
+    d.u = u;
+    d.p0 = p0;
+    return 1;
+}
+
 // sample.c:136-178 for a sampling row whose candidates (keys[0..t.total), ids) are in LDS:
 // radix-select the top K by logit, exact p, bitonic sort, prove the prefix, decide and
 // record; rows the proof does not cover go through full_row.  fcap bounds t.total,
@@ -1120,29 +1203,37 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
                 if (key_p(srt[j]) <= p_rej) atomicMin(&dl.sh[2], j);
         __syncthreads();
         const int E = min(m, dl.sh[2]);
-        if (tid == 0) {
+        if (tid < 64) {
             qs_pick_diag d;
             memset(&d, 0, sizeof d);
             uint64_t rs = st.rng[row];
             int id = -1;
-            if (decide_prefix(srt, E, t.nwin, P, rs, id, d)) {
-                st.rng[row] = rs;
-                ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
-                out[row] = id;
-                if (diag) {
-                    d.id = id;
-                    d.path = QS_PATH_FAST;
-                    d.n_window = t.nwin;
-                    d.n_cand = m;
-                    d.maxl = t.maxl;
-                    d.msc = msc;
-                    d.inv = inv;
-                    d.sum = t.sum;
-                    diag[row] = d;
+            int ok = -1;
+            if (npad <= 64) ok = decide_prefix_par<1>(srt, E, t.nwin, P, rs, id, d);
+            else if (npad <= 128) ok = decide_prefix_par<2>(srt, E, t.nwin, P, rs, id, d);
+            else if (npad <= 256) ok = decide_prefix_par<4>(srt, E, t.nwin, P, rs, id, d);
+            else if (npad <= 512) ok = decide_prefix_par<8>(srt, E, t.nwin, P, rs, id, d);
+            if (tid == 0) {
+                if (ok < 0) ok = decide_prefix(srt, E, t.nwin, P, rs, id, d) ? 1 : 0;
+                if (ok) {
+                    st.rng[row] = rs;
+                    ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
+                    out[row] = id;
+                    if (diag) {
+                        d.id = id;
+                        d.path = QS_PATH_FAST;
+                        d.n_window = t.nwin;
+                        d.n_cand = m;
+                        d.maxl = t.maxl;
+                        d.msc = msc;
+                        d.inv = inv;
+                        d.sum = t.sum;
+                        diag[row] = d;
+                    }
+                    dl.sh[0] = 0;
+                } else {
+                    dl.sh[0] = 1;
                 }
-                dl.sh[0] = 0;
-            } else {
-                dl.sh[0] = 1;
             }
         }
         __syncthreads();
