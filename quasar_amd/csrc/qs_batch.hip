@@ -876,8 +876,9 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
                                  d_out, d_diag, b->op_grid, b->stream);
     }
     if (b->mode == QS_MODE_PIPELINED || (b->mode == QS_MODE_AUTO && pipe_ok)) {
+        // top K above 64 on some row: the build whose block decision has the prefix sums
         return qs_pipe_launch(d_logits, row_stride, n_rows, n_vocab, st0, b->sc, d_out, d_diag,
-                              b->pipe_grid, b->stream);
+                              b->pipe_grid, kmax > 64 ? 1 : 0, b->stream);
     }
     Geometry g;
     g.logits = d_logits;

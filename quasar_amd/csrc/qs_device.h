@@ -1094,7 +1094,7 @@ __device__ __forceinline__ int decide_prefix_par(const uint64_t *srt, int E, int
 // record; rows the proof does not cover go through full_row.  fcap bounds t.total,
 // srt holds SC keys.  fixed_slot >= 0 names a full-window scratch slot owned by the
 // caller, -1 takes one under the slot locks.  All threads of the block call this.
-template <int NT, int SC = SORT_CAP>
+template <int NT, int SC = SORT_CAP, bool PAR = true>
 __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const RowTotals &t, int fcap,
                            uint32_t *keys, int32_t *ids, uint64_t *srt, DecideLds<NT> &dl,
                            FullLds<NT> &fl, const float *x, int V, const RowState &st,
@@ -1203,38 +1203,51 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
                 if (key_p(srt[j]) <= p_rej) atomicMin(&dl.sh[2], j);
         __syncthreads();
         const int E = min(m, dl.sh[2]);
-        if (tid < 64) {
+        // lane 0 records a decided row and sets dl.sh[0] to 0, or to 1 for the whole window
+        auto record = [&](bool ok, uint64_t rs, int id, qs_pick_diag &d) {
+            if (ok) {
+                st.rng[row] = rs;
+                ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
+                out[row] = id;
+                if (diag) {
+                    d.id = id;
+                    d.path = QS_PATH_FAST;
+                    d.n_window = t.nwin;
+                    d.n_cand = m;
+                    d.maxl = t.maxl;
+                    d.msc = msc;
+                    d.inv = inv;
+                    d.sum = t.sum;
+                    diag[row] = d;
+                }
+                dl.sh[0] = 0;
+            } else {
+                dl.sh[0] = 1;
+            }
+        };
+        if constexpr (PAR) {
+            if (tid < 64) {
+                qs_pick_diag d;
+                memset(&d, 0, sizeof d);
+                uint64_t rs = st.rng[row];
+                int id = -1;
+                int ok = -1;
+                if (npad <= 64) ok = decide_prefix_par<1>(srt, E, t.nwin, P, rs, id, d);
+                else if (npad <= 128) ok = decide_prefix_par<2>(srt, E, t.nwin, P, rs, id, d);
+                else if (npad <= 256) ok = decide_prefix_par<4>(srt, E, t.nwin, P, rs, id, d);
+                else if (npad <= 512) ok = decide_prefix_par<8>(srt, E, t.nwin, P, rs, id, d);
+                if (tid == 0) {
+                    if (ok < 0) ok = decide_prefix(srt, E, t.nwin, P, rs, id, d) ? 1 : 0;
+                    record(ok != 0, rs, id, d);
+                }
+            }
+        } else if (tid == 0) {
             qs_pick_diag d;
             memset(&d, 0, sizeof d);
             uint64_t rs = st.rng[row];
             int id = -1;
-            int ok = -1;
-            if (npad <= 64) ok = decide_prefix_par<1>(srt, E, t.nwin, P, rs, id, d);
-            else if (npad <= 128) ok = decide_prefix_par<2>(srt, E, t.nwin, P, rs, id, d);
-            else if (npad <= 256) ok = decide_prefix_par<4>(srt, E, t.nwin, P, rs, id, d);
-            else if (npad <= 512) ok = decide_prefix_par<8>(srt, E, t.nwin, P, rs, id, d);
-            if (tid == 0) {
-                if (ok < 0) ok = decide_prefix(srt, E, t.nwin, P, rs, id, d) ? 1 : 0;
-                if (ok) {
-                    st.rng[row] = rs;
-                    ring_record(ring, st.hlen + row, st.hhead + row, P.ring_cap, id);
-                    out[row] = id;
-                    if (diag) {
-                        d.id = id;
-                        d.path = QS_PATH_FAST;
-                        d.n_window = t.nwin;
-                        d.n_cand = m;
-                        d.maxl = t.maxl;
-                        d.msc = msc;
-                        d.inv = inv;
-                        d.sum = t.sum;
-                        diag[row] = d;
-                    }
-                    dl.sh[0] = 0;
-                } else {
-                    dl.sh[0] = 1;
-                }
-            }
+            const bool ok = decide_prefix(srt, E, t.nwin, P, rs, id, d);
+            record(ok, rs, id, d);
         }
         __syncthreads();
         full = dl.sh[0] != 0;
@@ -1370,7 +1383,7 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
 
 // decide_row with the one-wavefront decision first: all threads of the block call it,
 // with the gathered candidates in keys/ids (LDS) and the block synchronised.
-template <int NT, int SC = SORT_CAP>
+template <int NT, int SC = SORT_CAP, bool PAR = true>
 __device__ __forceinline__ void decide_row_fast(int row, const qs_row_param &P, const RowTotals &t,
                                                 int fcap, uint32_t *keys, int32_t *ids,
                                                 uint64_t *srt, DecideLds<NT> &dl,
@@ -1387,7 +1400,7 @@ __device__ __forceinline__ void decide_row_fast(int row, const qs_row_param &P, 
     const int status = dl.sh[7];
     __syncthreads();
     if (status == 1)
-        decide_row<NT, SC>(row, P, t, fcap, keys, ids, srt, dl, fl, x, V, st, sc, out, diag,
+        decide_row<NT, SC, PAR>(row, P, t, fcap, keys, ids, srt, dl, fl, x, V, st, sc, out, diag,
                            fixed_slot);
     else if (status == 2)
         full_row<NT>(x, V, row, P, t.maxl, t.sum, st, sc, out, diag, dl.tab, fl, fixed_slot);

@@ -65,4 +65,4 @@ int qs_pipe_parts(void);
 // Cooperative launch of the pipelined pick on `stream`.
 int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vocab,
                    const qs::RowState &st, const qs::Scratch &sc, int32_t *out,
-                   qs_pick_diag *diag, int grid, hipStream_t stream);
+                   qs_pick_diag *diag, int grid, int wide_k, hipStream_t stream);

@@ -684,6 +684,7 @@ __device__ __forceinline__ void control_release(const PipeArgs &a, int row) {
 }
 
 // Finish row r: gather its PARTS partial results and decide (all threads).
+template <bool PAR>
 __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t *dyn, PipeLds &pl, int slot) {
     const int tid = threadIdx.x, lane = tid & 63;
     const RowState &st = a.st;
@@ -775,7 +776,7 @@ __device__ __forceinline__ void finish_row(const PipeArgs &a, int row, uint32_t 
             }
         }
         __syncthreads();
-        decide_row_fast<NT>(row, P, t, FCAP, keys, ids, srt, pl.dl, fl, x, a.vocab, st, sc,
+        decide_row_fast<NT, SORT_CAP, PAR>(row, P, t, FCAP, keys, ids, srt, pl.dl, fl, x, a.vocab, st, sc,
                             a.out, a.diag, slot, &hist);
     }
     __syncthreads();
@@ -853,6 +854,10 @@ __device__ __forceinline__ void control_stage(int s, RowFetch &rp, const PipeArg
     if (rel) control_release(a, rs);              // the stores completed before the poll
 }
 
+// PAR: the block decision takes the wavefront prefix sums where they are exact (rows with
+// top K above 64).  Without it that code stays out of the kernel, whose register
+// allocation the stages feel; both give the same results.
+template <bool PAR>
 __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     extern __shared__ __align__(16) uint32_t dyn[];
     __shared__ PipeLds pl;
@@ -951,7 +956,7 @@ __global__ void __launch_bounds__(NT) k_pipe(PipeArgs a) {
     }
     __syncthreads();
     // epilogue: rows r = w (mod G), each with this workgroup's full-window slot
-    for (int r = w; r < a.n_rows; r += gridDim.x) finish_row(a, r, dyn, pl, w);
+    for (int r = w; r < a.n_rows; r += gridDim.x) finish_row<PAR>(a, r, dyn, pl, w);
 }
 
 }  // namespace
@@ -987,7 +992,7 @@ int qs_pipe_grid(int max_vocab) {
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_pipe, NT, qs_pipe_lds_bytes(max_vocab)) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_pipe<true>, NT, qs_pipe_lds_bytes(max_vocab)) !=
             hipSuccess ||
         nb < 1)
         return 0;
@@ -996,7 +1001,7 @@ int qs_pipe_grid(int max_vocab) {
 
 int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vocab,
                    const RowState &st, const Scratch &sc, int32_t *out, qs_pick_diag *diag,
-                   int grid, hipStream_t stream) {
+                   int grid, int wide_k, hipStream_t stream) {
     PipeArgs a;
     a.logits = logits;
     a.stride = row_stride;
@@ -1009,7 +1014,10 @@ int qs_pipe_launch(const float *logits, int64_t row_stride, int n_rows, int n_vo
     a.sc = sc;
     a.out = out;
     a.diag = diag;
-    hipLaunchKernelGGL(k_pipe, dim3(grid), dim3(NT), qs_pipe_lds_bytes(n_vocab), stream, a);
+    if (wide_k)
+        hipLaunchKernelGGL(k_pipe<true>, dim3(grid), dim3(NT), qs_pipe_lds_bytes(n_vocab), stream, a);
+    else
+        hipLaunchKernelGGL(k_pipe<false>, dim3(grid), dim3(NT), qs_pipe_lds_bytes(n_vocab), stream, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         qs_set_error("k_pipe launch: %s", hipGetErrorString(e));
