@@ -86,6 +86,11 @@ STRESS = {
     "minp_only_b8": Workload(
         "minp_only_b8", 8, DIST_NORMAL, 2.0, 0.0, 1.0, 1.0, 0, 0.1, 1.2, 64, 64, 0, 0xD3,
         description="top-k and top-p off, min-p 0.1, penalty 1.2"),
+    "peaked_tail_b64": Workload(
+        "peaked_tail_b64", 64, DIST_NORMAL_PEAK, 2.0, 30.0, 1.0, 1.0, 300, 0.0, 1.0, 0, 0, 0,
+        0xD4,
+        description="one column 30 above N(0, 2.0), top-k 300, top-p and min-p off: the "
+                    "draw sums 300 probabilities, most of them below 2^-29"),
 }
 
 BENCH_WORKLOAD = "peaked_b256"

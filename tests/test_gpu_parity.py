@@ -201,6 +201,7 @@ def run_batch_vs_oracle(qa, oracle, w, rows_checked, picks=1):
     ("nucleus_b8", None, 1),
     ("fullwindow_b8", None, 1),
     ("minp_only_b8", None, 2),
+    ("peaked_tail_b64", None, 2),
 ])
 def test_workload_batch_vs_cpu(qa, oracle, name, rows, picks):
     w = allw()[name]
