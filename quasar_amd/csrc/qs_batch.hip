@@ -469,7 +469,7 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
         }
     }
     __syncthreads();
-    decide_row_fast<WG>(row, P, t, FIN_CAP, keys, ids, srt, dl, fl, x, g.vocab, st, sc, a.out,
+    decide_row_fast<WG, SORT_CAP, true>(row, P, t, FIN_CAP, keys, ids, srt, dl, fl, x, g.vocab, st, sc, a.out,
                         a.diag, -1);
 }
 

@@ -1093,8 +1093,10 @@ __device__ __forceinline__ int decide_prefix_par(const uint64_t *srt, int E, int
 // radix-select the top K by logit, exact p, bitonic sort, prove the prefix, decide and
 // record; rows the proof does not cover go through full_row.  fcap bounds t.total,
 // srt holds SC keys.  fixed_slot >= 0 names a full-window scratch slot owned by the
-// caller, -1 takes one under the slot locks.  All threads of the block call this.
-template <int NT, int SC = SORT_CAP, bool PAR = true>
+// caller, -1 takes one under the slot locks.  All threads of the block call this.  PAR:
+// the cuts and the draw come from decide_prefix_par where its sums are exact (same
+// results; more code in the caller's kernel).
+template <int NT, int SC = SORT_CAP, bool PAR = false>
 __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const RowTotals &t, int fcap,
                            uint32_t *keys, int32_t *ids, uint64_t *srt, DecideLds<NT> &dl,
                            FullLds<NT> &fl, const float *x, int V, const RowState &st,
@@ -1383,7 +1385,7 @@ __device__ __forceinline__ int decide_row_wave(int row, const qs_row_param &P, c
 
 // decide_row with the one-wavefront decision first: all threads of the block call it,
 // with the gathered candidates in keys/ids (LDS) and the block synchronised.
-template <int NT, int SC = SORT_CAP, bool PAR = true>
+template <int NT, int SC = SORT_CAP, bool PAR = false>
 __device__ __forceinline__ void decide_row_fast(int row, const qs_row_param &P, const RowTotals &t,
                                                 int fcap, uint32_t *keys, int32_t *ids,
                                                 uint64_t *srt, DecideLds<NT> &dl,
