@@ -576,6 +576,59 @@ __device__ __forceinline__ void wave_sort_lds_desc(uint64_t *s, int n) {
         if (q * 64 + lane < n) s[q * 64 + lane] = v[q];
 }
 
+// One direction of a bitonic merge over a wavefront's 64 keys (strides 32 down to 1).
+__device__ __forceinline__ uint64_t wave_merge_dir(uint64_t v, bool desc, int lane) {
+    auto step = [&](uint64_t o, int S) {
+        const bool keep_max = ((lane & S) == 0) == desc;
+        v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
+    };
+    step(xor_lane64<32>(v), 32);
+    step(xor_lane64<16>(v), 16);
+    step(xor_lane64<8>(v), 8);
+    step(xor_lane64<4>(v), 4);
+    step(xor_lane64<2>(v), 2);
+    step(xor_lane64<1>(v), 1);
+    return v;
+}
+
+// bitonic_desc's network over s[0, 64*W) with W = n/64 wavefronts (n a power of two,
+// 128 <= n <= NT): element i in lane i%64 of wavefront i/64; strides below 64 move
+// between lanes, larger ones through s with a barrier pair.  Every thread of the block
+// calls this; s[0, n) ends sorted descending.
+template <int NT>
+__device__ __forceinline__ void block_sort_desc_waves(uint64_t *s, int n) {
+    const int i = threadIdx.x, lane = i & 63, w = i >> 6;
+    const bool part = i < n;
+    uint64_t v = 0ull;
+    if (part) {
+        v = s[i];
+        bitonic_step<2, 1>(v, lane);
+        bitonic_step<4, 2>(v, lane);   bitonic_step<4, 1>(v, lane);
+        bitonic_step<8, 4>(v, lane);   bitonic_step<8, 2>(v, lane);   bitonic_step<8, 1>(v, lane);
+        bitonic_step<16, 8>(v, lane);  bitonic_step<16, 4>(v, lane);  bitonic_step<16, 2>(v, lane);
+        bitonic_step<16, 1>(v, lane);
+        bitonic_step<32, 16>(v, lane); bitonic_step<32, 8>(v, lane);  bitonic_step<32, 4>(v, lane);
+        bitonic_step<32, 2>(v, lane);  bitonic_step<32, 1>(v, lane);
+        v = wave_merge_dir(v, (w & 1) == 0, lane);              // size 64
+    }
+    for (int size = 128; size <= n; size <<= 1) {
+        for (int S = size >> 1; S >= 64; S >>= 1) {
+            __syncthreads();                                     // last exchange read
+            if (part) s[i] = v;
+            __syncthreads();
+            if (part) {
+                const uint64_t o = s[i ^ S];
+                const bool keep_max = ((i & S) == 0) == ((i & size) == 0);
+                v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
+            }
+        }
+        if (part) v = wave_merge_dir(v, (i & size) == 0, lane);
+    }
+    __syncthreads();
+    if (part) s[i] = v;
+    __syncthreads();
+}
+
 // (p, id) sort key: p's bits above, ~id below, so descending order is p desc, id asc
 // (sample.c:151 under glibc's stable merge sort on ascending ids).
 __device__ __forceinline__ uint64_t pid_key(float p, int id) {
@@ -1173,7 +1226,9 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
         while (npad < nkept) npad <<= 1;
         for (int j = nkept + tid; j < npad; j += NT) srt[j] = 0ull;
         __syncthreads();
-        if (npad <= 512) {                          // one wavefront, no barriers
+        if (npad >= 128 && npad <= 512 && npad <= NT) {
+            block_sort_desc_waves<NT>(srt, npad);       // npad / 64 wavefronts
+        } else if (npad <= 512) {                   // one wavefront, no barriers
             if (tid < 64) {
                 if (npad <= 64) wave_sort_lds_desc<1>(srt, npad);
                 else if (npad <= 128) wave_sort_lds_desc<2>(srt, npad);
