@@ -136,9 +136,11 @@ def host_cpu():
 
 
 def cpu_baseline(w, logits_host, hist, seeds, gpu_ids, gpu_diag, args):
-    """Time the reference sampler (or the restatement) on the host over whole copies of
-    the batch until about args.cpu_seconds of work, on up to 16 threads and on one; check
-    the GPU's first-step ids and intermediates against the restatement on every row."""
+    """Time the reference sampler (or the restatement) on the host: one untimed warm-up
+    pass, then at least 5 timed passes (until about args.cpu_seconds of work), on as many
+    threads as the process may use (nproc) and on one; the rate is the median pass's.
+    Check the GPU's first-step ids and intermediates against the restatement on every
+    row."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from pyoracle import Oracle, Params, RefSampler, parity_report
     if RefSampler.available():
@@ -147,30 +149,32 @@ def cpu_baseline(w, logits_host, hist, seeds, gpu_ids, gpu_diag, args):
         impl, kind = Oracle(), "port"
     p = Params(*[w.temperature, w.top_p, w.min_p, w.repeat_penalty], w.top_k, w.repeat_last_n)
     usable, host_cpus, model = host_cpu()
-    threads = args.cpu_threads or min(usable, 16)
+    threads = args.cpu_threads or usable
     B, V = logits_host.shape
 
     def timed(n_threads, rows, budget):
-        done, secs, reps = 0, 0.0, 0
-        while True:
+        """(median rows/s over the timed passes, rows per pass, passes, seconds)"""
+        impl.pick_rows(p, logits_host, rows, V, hist, seeds, n_threads)    # warm-up
+        rates, secs = [], 0.0
+        while len(rates) < 5 or (secs < budget and len(rates) < 200):
             _, s_ = impl.pick_rows(p, logits_host, rows, V, hist, seeds, n_threads)
-            done += rows
+            rates.append(rows / s_)
             secs += s_
-            reps += 1
-            if secs >= budget or reps >= 200:
-                return done / secs, done, secs, reps
+        return float(np.median(rates)), rows, len(rates), secs
 
-    rate, done, secs, reps = timed(threads, B, args.cpu_seconds)
-    one_rows = max(1, min(B, int(rate / threads * args.cpu_seconds / 4)))
-    rate1, done1, secs1, _ = timed(1, one_rows, args.cpu_seconds / 4)
+    rate, _, reps, secs = timed(threads, B, args.cpu_seconds)
+    # one core: passes of about a fifth of a quarter of the budget each
+    one_rows = max(1, min(B, int(rate / threads * args.cpu_seconds / 20)))
+    rate1, _, reps1, secs1 = timed(1, one_rows, args.cpu_seconds / 4)
     orc_ids, orc_diag, _ = Oracle().pick_rows_diag(p, logits_host, B, V, hist, seeds, threads)
     parity = parity_report(gpu_ids, gpu_diag, orc_ids, orc_diag)
-    return {"value": rate, "unit": "rows/s", "cores": threads, "kind": kind,
+    base = {"value": rate, "unit": "rows/s", "cores": threads, "kind": kind,
             "single_core": rate1, "host_cpus": host_cpus, "cpu_model": model,
-            "sample": f"{reps} pass(es) over all {B} rows of {w.name} ({done} picks, "
-                      f"{secs:.1f} s of pick time summed over the slowest thread) on "
-                      f"{threads} POSIX threads, one sampler per row; single core: the "
-                      f"first {one_rows} rows, {done1} picks in {secs1:.1f} s"}, parity
+            "sample": f"median of {reps} timed passes (after one warm-up pass) over all {B} "
+                      f"rows of {w.name} ({secs:.1f} s of pick time) on {threads} POSIX "
+                      f"threads (nproc {usable}), one sampler per row; single core: median "
+                      f"of {reps1} passes over the first {one_rows} rows ({secs1:.1f} s)"}
+    return base, parity
 
 
 def router_bench(args):

@@ -174,7 +174,7 @@ __global__ void __launch_bounds__(WG) k_scan(Geometry g, RowState st, Scratch sc
 
     const int slice = blockIdx.x, row = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const qs_row_param P = st.prm[row];
+    const qs_row_param P = row_param(st, row);
     const bool greedy = row_greedy(P);
     const int lo = slice * g.slice_len;
     const int hi = min(lo + g.slice_len, g.vocab);
@@ -298,7 +298,7 @@ __global__ void __launch_bounds__(WG) k_expsum(Geometry g, RowState st, Scratch 
 
     const int slice = blockIdx.x, row = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const qs_row_param P = st.prm[row];
+    const qs_row_param P = row_param(st, row);
     if (row_greedy(P)) return;
     const int li = row * g.slices + slice;
 
@@ -389,7 +389,7 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
     const Geometry &g = a.g;
     const Scratch &sc = a.sc;
     const RowState &st = a.st;
-    const qs_row_param P = st.prm[row];
+    const qs_row_param P = row_param(st, row);
     const int S = g.slices;
     const int l0 = row * S;
     if (tid < QS_EXPF_TAB_N) dl.tab[tid] = c_exp_tab[tid];
@@ -570,6 +570,8 @@ struct qs_batch {
     Scratch sc{};
     HeadRec *d_hrec = nullptr;             // the output layer's per-(row, tile) records
     uint32_t *d_hbits = nullptr;           // its history bitmap (zero between picks)
+    bool hbits_dirty = false;              // a fused pick failed after marking it: clear
+                                           // it before the next one
 };
 
 static void batch_release(qs_batch *b) {
@@ -985,6 +987,14 @@ static int head_check(qs_batch *b, const void *d_hidden, const void *d_weight, i
             return rc;
         }
     }
+    if (b->hbits_dirty) {
+        // the bitmap kernel of a failed fused pick may have left bits that only the output
+        // layer's kernel clears
+        HIP_TRY(hipStreamSynchronize(b->stream), "sync");
+        HIP_TRY(hipMemset(b->d_hbits, 0, sizeof(uint32_t) * (QS_HEAD_MAX_ROWS / 32) *
+                                             (size_t)b->max_vocab), "clearing the history bits");
+        b->hbits_dirty = false;
+    }
     int kmax = 1;
     bool any = false;
     return batch_kmax(b, n_rows, &kmax, &any);
@@ -1010,8 +1020,10 @@ int qs_batch_pick_head(qs_batch *b, const void *d_hidden, const void *d_weight, 
         return rc;
     RowState st{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
                 b->max_last_n > 0 ? b->max_last_n : 1};
-    return qs_head_launch(d_hidden, d_weight, n_embd, n_rows, n_vocab, d_logits, st, b->sc,
-                          b->d_hrec, b->d_hbits, d_out, d_diag, b->stream);
+    const int rc = qs_head_launch(d_hidden, d_weight, n_embd, n_rows, n_vocab, d_logits, st,
+                                  b->sc, b->d_hrec, b->d_hbits, d_out, d_diag, b->stream);
+    if (rc) b->hbits_dirty = true;
+    return rc;
 }
 
 size_t qs_head_packed_bytes(int n_embd, int n_vocab) {

@@ -90,7 +90,9 @@ __device__ __forceinline__ void row_visit(const PartArgs &a, int row, const qs_r
                                           DecLds &dl, F &&f) {
     const int tid = threadIdx.x;
     const float rp = P.repeat_penalty;
-    const int len = a.st.hlen[row], head = a.st.hhead[row], cap = P.ring_cap;
+    const int cap = P.ring_cap;                   // (clamped: row_param)
+    int len, head;
+    ring_pos(a.st, row, cap, len, head);
     const bool pen = rp > 1.0f && len > 0 && cap > 0;
     const int32_t *ring = a.st.ring + (int64_t)row * a.st.ring_stride;
     const float4 *x4 = (const float4 *)(a.logits + (int64_t)row * a.stride);
@@ -100,7 +102,7 @@ __device__ __forceinline__ void row_visit(const PartArgs &a, int row, const qs_r
             for (int j = tid; j < bitmap_words(XBM); j += ND) dl.bm[j] = 0u;
             __syncthreads();
             for (int j = tid; j < len; j += ND) {
-                const int id = ring[(head + j) % cap];
+                const int id = ring[qs_ring_slot(cap, head, j)];
                 if (id >= lo && id < hi) atomicOr(&dl.bm[(id - lo) >> 5], 1u << ((id - lo) & 31));
             }
             __syncthreads();

@@ -16,6 +16,7 @@
 #include "../../include/quasar_sampler.h"
 #include "qs_expf.h"
 #include "qs_internal.h"
+#include "qs_ring.h"
 
 namespace qs {
 
@@ -392,30 +393,21 @@ __device__ __forceinline__ double rng_unit(uint64_t &st) {
     return (double)((x * 0x2545F4914F6CDD1Dull) >> 11) * (1.0 / 9007199254740992.0);
 }
 
-// sample.c:83-92: append, or overwrite the oldest once the ring is full.
-// With the row's history length and head already loaded (len, head).
+// sample.c:83-92: append, or overwrite the oldest once the ring is full (qs_ring_put;
+// `cap` is the row's clamped capacity, row_param).  With the row's history length and head
+// already loaded (len, head).
 __device__ __forceinline__ void ring_record_at(int32_t *ring, int32_t *hlen, int32_t *hhead,
                                                int cap, int id, int len, int head) {
-    if (cap <= 0) return;
-    if (len < cap) {
-        ring[(head + len) % cap] = id;
-        *hlen = len + 1;
-    } else {
-        ring[head] = id;
-        *hhead = (head + 1) % cap;
-    }
+    const int s = qs_ring_put(cap, &len, &head);
+    if (s < 0) return;
+    ring[s] = id;
+    *hlen = len;
+    *hhead = head;
 }
 __device__ __forceinline__ void ring_record(int32_t *ring, int32_t *hlen, int32_t *hhead,
                                             int cap, int id) {
     if (cap <= 0) return;
-    const int len = *hlen, head = *hhead;
-    if (len < cap) {
-        ring[(head + len) % cap] = id;
-        *hlen = len + 1;
-    } else {
-        ring[head] = id;
-        *hhead = (head + 1) % cap;
-    }
+    ring_record_at(ring, hlen, hhead, cap, id, *hlen, *hhead);
 }
 
 __host__ __device__ __forceinline__ bool row_greedy(const qs_row_param &p) {
@@ -438,6 +430,21 @@ struct RowState {
     int32_t *hhead;
     int ring_stride;
 };
+
+// A row's stored parameters with its ring capacity clamped to the ring's storage
+// (qs_ring_cap): every kernel loads them through this.
+__device__ __forceinline__ qs_row_param row_param(const RowState &st, int row) {
+    qs_row_param P = st.prm[row];
+    P.ring_cap = qs_ring_cap(P.ring_cap, st.ring, st.ring_stride);
+    return P;
+}
+// A row's history length and head, clamped to `cap` (the row's clamped capacity).
+__device__ __forceinline__ void ring_pos(const RowState &st, int row, int cap, int &len,
+                                         int &head) {
+    len = st.hlen[row];
+    head = st.hhead[row];
+    qs_ring_clamp(cap, &len, &head);
+}
 
 // One wavefront's results for one part in the streaming kernel (32 bytes).
 struct WaveRec {
@@ -490,10 +497,11 @@ __device__ __forceinline__ void build_bitmap(uint32_t *bm, int words, int lo, in
                              int row, int cap) {
     for (int j = threadIdx.x; j < words; j += NT) bm[j] = 0u;
     __syncthreads();
-    const int len = st.hlen[row], head = st.hhead[row];
+    int len, head;
+    ring_pos(st, row, cap, len, head);
     const int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
     for (int j = threadIdx.x; j < len; j += NT) {
-        const int id = ring[(head + j) % cap];
+        const int id = ring[qs_ring_slot(cap, head, j)];
         if (id >= lo && id < hi) atomicOr(&bm[(id - lo) >> 5], 1u << ((id - lo) & 31));
     }
     __syncthreads();

@@ -156,12 +156,14 @@ __device__ __forceinline__ double row16_sum_d(double v) {
 __global__ void __launch_bounds__(256) k_head_prep(HeadArgs a) {
     const int row = blockIdx.x;
     const RowState &st = a.st;
-    const qs_row_param P = st.prm[row];
-    const int len = st.hlen[row], head = st.hhead[row], cap = P.ring_cap;
+    const qs_row_param P = row_param(st, row);
+    const int cap = P.ring_cap;
+    int len, head;
+    ring_pos(st, row, cap, len, head);
     if (!(P.repeat_penalty > 1.0f) || len <= 0 || cap <= 0) return;
     const int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
     for (int j = threadIdx.x; j < len; j += 256) {
-        const int id = ring[(head + j) % cap];
+        const int id = ring[qs_ring_slot(cap, head, j)];
         if (id >= 0 && id < a.V) atomicOr(&a.hb[(int64_t)(row >> 5) * a.V + id], 1u << (row & 31));
     }
 }
@@ -392,7 +394,7 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
     DecLds &dl = HL.d;
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const RowState &st = a.st;
-    const qs_row_param P = st.prm[row];
+    const qs_row_param P = row_param(st, row);
     const bool greedy = row_greedy(P);
     const int NT_ = a.ntiles, V = a.V;
     const float *x = a.logits + (int64_t)row * V;
@@ -410,10 +412,12 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
     }
     // the first ND history ids, requested with the records
     const float rp = P.repeat_penalty;
-    const int len = st.hlen[row], head = st.hhead[row], cap = P.ring_cap;
+    const int cap = P.ring_cap;
+    int len, head;
+    ring_pos(st, row, cap, len, head);
     const bool pen = rp > 1.0f && len > 0 && cap > 0;
     const int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
-    const int hid0 = pen && tid < len ? ring[(head + tid) % cap] : -1;
+    const int hid0 = pen && tid < len ? ring[qs_ring_slot(cap, head, tid)] : -1;
     mk = wave_max_u(mk);
     if (lane == 0) dl.exc[wv] = (int)mk;
     __syncthreads();
@@ -528,7 +532,7 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
     const double rinv = 1.0 / (double)rp;
     if (pen) {
         for (int j = tid; j < len; j += ND) {
-            const int id = j == tid ? hid0 : ring[(head + j) % cap];
+            const int id = j == tid ? hid0 : ring[qs_ring_slot(cap, head, j)];
             if (id >= 0 && id < V) {
                 const int s = HL.sel[id / HT];
                 if (s >= 0) atomicOr(&HL.selbits[s][(id % HT) >> 5], 1u << (id & 31));
@@ -658,7 +662,11 @@ int qs_head_launch(const void *d_hidden, const void *d_weight, int n_embd, int n
     a.st = st;
     if (a.records) {
         hipLaunchKernelGGL(k_head_prep, dim3((unsigned)n_rows), dim3(256), 0, stream, a);
-        if (hipGetLastError() != hipSuccess) return QS_EDEVICE;
+        const hipError_t ep = hipGetLastError();
+        if (ep != hipSuccess) {
+            qs_set_error("head history bitmap launch: %s", hipGetErrorString(ep));
+            return QS_EDEVICE;
+        }
     }
     // the smallest row capacity that holds the batch (a deeper ring for fewer rows)
     if (n_rows <= 64)

@@ -122,8 +122,11 @@ int qs_pick_noalloc(const float *d_logits, int64_t row_stride, int n_rows, int n
     sc.ccap = 0;
     sc.spin_limit = SPIN_LIMIT;
     static_assert(sizeof(qs_row_config) == sizeof(qs_row_param), "row config layout");
-    RowState st{(const qs_row_param *)d_config, d_rng, d_ring, d_hist_len, d_hist_head,
-                ring_stride > 0 ? ring_stride : 1};
+    // the kernels clamp each row's ring capacity to ring_stride (0: no ring, whatever the
+    // row configs say) and its history length and head to that capacity (qs_ring.h), so
+    // the caller's state arrays never send an access outside a row's own ring
+    RowState st{(const qs_row_param *)d_config, d_rng, ring_stride > 0 ? d_ring : nullptr,
+                d_hist_len, d_hist_head, ring_stride};
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(k_zero, dim3(1), dim3(64), 0, s, sc.locks, QS_NOALLOC_SLOTS + 1);
     hipError_t e = hipGetLastError();

@@ -209,11 +209,10 @@ __device__ __forceinline__ void lds_or(uint32_t *p, uint32_t v) {
 // penalised once).
 __device__ __forceinline__ void bitmap_mark(uint32_t *bm, uint32_t *hitw, const StreamArgs &a,
                                             const Loc &l, int slot, int cap) {
-    const int len = a.hlen[l.row], head = a.hhead[l.row];
+    int len = a.hlen[l.row], head = a.hhead[l.row];
+    qs_ring_clamp(cap, &len, &head);
     auto mark = [&](int p, int id) {
-        int d = p - head;
-        if (d < 0) d += cap;
-        if (p < cap && d < len && id >= l.lo && id < l.hi) {
+        if (qs_ring_live(cap, len, head, p) && id >= l.lo && id < l.hi) {
             const int q = id - l.lo, c = q >> 2, u = c / NT;   // float4 c: thread c - u*NT
             lds_or(&bm[q >> 5], 1u << (q & 31));
             lds_or(&hitw[(c - u * NT) >> 6], 1u << u);
@@ -232,8 +231,15 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// A row's parameters with its ring capacity clamped to the ring's storage (qs_ring_cap).
+__device__ __forceinline__ qs_row_param stream_param(const StreamArgs &a, int row) {
+    qs_row_param P = a.prm[row];
+    P.ring_cap = qs_ring_cap(P.ring_cap, a.ring, a.ring_stride);
+    return P;
+}
 // The ring capacity whose ids a row's bitmap marks: none without a penalty (sample.c:119).
-__device__ __forceinline__ int mark_cap(const qs_row_param &P) {
+__device__ __forceinline__ int mark_cap(const StreamArgs &a, int row) {
+    const qs_row_param P = stream_param(a, row);
     return P.repeat_penalty > 1.0f ? P.ring_cap : 0;
 }
 // All threads: zero a bitmap slot and its hit masks.
@@ -479,12 +485,12 @@ k_part(StreamArgs sa, const float *__restrict__ logits, const qs_row_param *__re
     issue_stage(stage0, a, cur);
     for (int s = 0; s < 3; ++s) bitmap_zero(pl.bm[s], pl.hitw[s]);
     lds_barrier();
-    bitmap_mark(pl.bm[0], pl.hitw[0], a, cur, ring0, mark_cap(a.prm[cur.row]));
+    bitmap_mark(pl.bm[0], pl.hitw[0], a, cur, ring0, mark_cap(a, cur.row));
     if (run.begin + 1 < run.end) {
         const Loc n1 = loc_next(a, run, cur);
         const int ring1 = ring_slot(a, n1.row);
         if constexpr (STAGES > 1) issue_stage(stage1, a, n1);
-        bitmap_mark(pl.bm[1], pl.hitw[1], a, n1, ring1, mark_cap(a.prm[n1.row]));
+        bitmap_mark(pl.bm[1], pl.hitw[1], a, n1, ring1, mark_cap(a, n1.row));
     }
     lds_barrier();
     const int tid = tix();
@@ -517,14 +523,14 @@ k_part(StreamArgs sa, const float *__restrict__ logits, const qs_row_param *__re
             }
             if constexpr (STAGES == 1) issue_stage(stage, a, n1);
         }
-        const qs_row_param P = a.prm[cur.row];
+        const qs_row_param P = stream_param(a, cur.row);
         const int s2 = s0 == 0 ? 2 : s0 - 1;          // (s0 + 2) mod 3
         part_step(X, a, cur, P, pl.bm[s0], pl.hitw[s0], (idx - run.begin) & 1, pl, [&] {
             // slot s0 was read by this part's pass 1 (done): cleared for part idx + 3;
             // slot s2 (cleared a part ago) gets part idx + 2's ids
             bitmap_zero(pl.bm[s0], pl.hitw[s0]);
             if (more2) bitmap_mark(pl.bm[s2], pl.hitw[s2], a, n2, ring_val,
-                                   mark_cap(a.prm[n2.row]));
+                                   mark_cap(a, n2.row));
         }, tl);
         prev = cur;
         cur = n1;
@@ -738,7 +744,7 @@ __global__ void __launch_bounds__(ND) k_decide(PartArgs a) {
     const int NP = a.parts;
     const int NL = NP * NWV;                          // candidate lists: NWV per part
     const int l0 = row * NP;
-    const qs_row_param P = st.prm[row];
+    const qs_row_param P = row_param(st, row);
     const bool greedy = row_greedy(P);
     const float *x = a.logits + (int64_t)row * a.stride;
     if (tid < QS_EXPF_TAB_N) dl.dl.tab[tid] = c_tab_part[tid];

@@ -168,7 +168,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     TL_ROW(0);
-    const qs_row_param P = a.st.prm[row];
+    const qs_row_param P = row_param(a.st, row);
 #ifdef QS_TIMELINE
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     QS_TL_HOOK(12);
@@ -197,11 +197,12 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
     int jA = wv, jB = NW + wv;
     if (nr < nch && wv == NW - 1) load_chunk(T, rs, nr, lane);
     load_chunk(A, rs, jA, lane);
-    const int cap = P.repeat_penalty > 1.0f ? min(P.ring_cap, a.st.ring_stride) : 0;   // sample.c:119
+    const int cap = P.repeat_penalty > 1.0f ? P.ring_cap : 0;   // sample.c:119 (clamped: row_param)
     const uint64_t tabv = tid < QS_EXPF_TAB_N ? c_tab_row[tid] : 0ull;
     RowHist hist{0ull, 0, 0};
     if (wv == 0 && !greedy) hist = row_hist(a.st, row);
-    const int hlen = a.st.hlen[row], hhead = a.st.hhead[row];
+    int hlen, hhead;
+    ring_pos(a.st, row, cap, hlen, hhead);
     const float x0 = rowp[0];
     // the history bitmap and each chunk's hit bit
     const int bw = ((n4 + 7) / 8 + 3) / 4;       // uint4s of bitmap words in use
@@ -224,9 +225,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
     lds_barrier();
     QS_TL_HOOK(14);
     auto mark = [&](int p, int id) {
-        int d = p - hhead;
-        if (d < 0) d += cap;
-        if (p < cap && d < hlen && id >= 0 && id < V) {   // each id once (a bit)
+        if (qs_ring_live(cap, hlen, hhead, p) && id >= 0 && id < V) {   // each id once (a bit)
             atomicOr(&rl.bm[id >> 5], 1u << (id & 31));
             const int f = id >> 2, ch = f / RCH, r = f - ch * RCH;
             atomicOr(&rl.hitu[ch], 1u << (r >> 6));

@@ -11,7 +11,9 @@
  * when the device cannot take the pick (no device memory, no GPU, a device error), records
  * the id and reports it once on stderr.  The history is mirrored on the host for that
  * (each returned id is appended, sample.c:83-92), so the device row can be rebuilt from
- * it at the next pick. */
+ * it at the next pick.  The generator state is mirrored the same way (one xorshift64 step
+ * per sampling pick, none for a greedy one or the fallback, sample.c:130-134,170), so a
+ * lost device row is rebuilt from the state the reference would hold. */
 #define _POSIX_C_SOURCE 200809L
 #include <stdio.h>
 #include <stdlib.h>
@@ -29,7 +31,7 @@ struct quasar_sampler {
     /* Host copy of the configuration, to re-apply when the batch is re-created and to
      * seed it when a config arrives before the first pick. */
     qs_row_param  prm;
-    uint64_t      rng;          /* generator state as last known on the host */
+    uint64_t      rng;          /* generator state, mirrored on the host */
     /* Host mirror of the history ring, sample.c's hist/hist_cap/hist_len/hist_head. */
     int32_t      *hist;
     int           hist_cap, hist_len, hist_head;
@@ -46,6 +48,14 @@ static void host_record(quasar_sampler *s, int id) {
         s->hist[s->hist_head] = id;
         s->hist_head = (s->hist_head + 1) % s->hist_cap;
     }
+}
+
+/* sample.c:72-77: the generator's step; a sampling pick takes one (sample.c:170). */
+static uint64_t host_xorshift(uint64_t x) {
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    return x;
 }
 
 /* The mirror's ids oldest first into out[hist_len]. */
@@ -179,6 +189,7 @@ int quasar_sampler_pick(quasar_sampler *s, const float *logits, int n_vocab) {
     if (rc == 0 && (id < 0 || id >= n_vocab)) rc = QS_EDEVICE;
     if (rc == 0) {
         host_record(s, id);
+        if (!(s->prm.temperature <= 0.0f)) s->rng = host_xorshift(s->rng);   /* sample.c:130 */
         return id;
     }
     /* The device could not take the pick: the reference's out-of-memory answer. */
@@ -217,12 +228,20 @@ int qs_sampler_get_state(const quasar_sampler *s, uint64_t *rng, int32_t *hist, 
     }
     *rng = s->rng;
     if (s->batch) {
+        /* the device's state, which the host mirror must equal */
         int32_t *tmp = (int32_t *)malloc(sizeof(int32_t) * (size_t)(s->ring_cap > 0 ? s->ring_cap : 1));
         int len = 0;
+        uint64_t dev = 0;
         if (!tmp) return QS_ENOMEM;
-        const int rc = qs_batch_get_state(s->batch, 0, rng, tmp, s->ring_cap, &len);
+        const int rc = qs_batch_get_state(s->batch, 0, &dev, tmp, s->ring_cap, &len);
         free(tmp);
         if (rc != 0) return rc;
+        if (dev != s->rng) {
+            qs_set_error("qs_sampler_get_state: device generator state %llx differs from the "
+                         "host mirror %llx", (unsigned long long)dev,
+                         (unsigned long long)s->rng);
+            return QS_EDEVICE;
+        }
     }
     const int n = s->hist_len < hist_cap ? s->hist_len : hist_cap;
     int32_t *all = (int32_t *)malloc(sizeof(int32_t) * (size_t)(s->hist_len > 0 ? s->hist_len : 1));
