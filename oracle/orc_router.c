@@ -31,6 +31,19 @@ static void orc_softmax(float *a, int n) {
     for (int i = 0; i < n; i++) a[i] *= inv;
 }
 
+/* The softmax of one row as orc_softmax leaves it (p[n]) and the float sum of its
+ * numerators (for the tests' bounds on it). */
+void orc_router_probs(const float *x, int n, float *p, float *sum_out) {
+    float mx = x[0];
+    for (int i = 1; i < n; i++)
+        if (x[i] > mx) mx = x[i];
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) sum += expf(x[i] - mx);
+    for (int i = 0; i < n; i++) p[i] = x[i];
+    orc_softmax(p, n);
+    *sum_out = sum;
+}
+
 /* forward_cpu.c:296-304, token by token.  n_expert <= 256, n_used <= 64. */
 void orc_router_topk(const float *logits, long row_stride, int n_tokens, int n_expert,
                      int n_used, int norm_topk, int32_t *idx, float *wt) {

@@ -107,6 +107,8 @@ long  orc_check_expf_range(float lo, float hi, int n_threads);
  * (orc_router.c): idx/wt hold n_used slots per token. */
 void orc_router_topk(const float *logits, long row_stride, int n_tokens, int n_expert,
                      int n_used, int norm_topk, int32_t *idx, float *wt);
+/* One row's softmax (forward_cpu.c:165-172) and the float sum of its numerators. */
+void orc_router_probs(const float *x, int n, float *p, float *sum_out);
 
 #ifdef __cplusplus
 }

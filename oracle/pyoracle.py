@@ -198,6 +198,7 @@ class Oracle:
         lib.orc_check_expf_range.restype = C.c_long
         lib.orc_router_topk.argtypes = [_F, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int, _I,
                                         _F]
+        lib.orc_router_probs.argtypes = [_F, C.c_int, _F, _F]
 
     def router_topk(self, logits, n_used, norm_topk):
         """forward_cpu.c:165-172, 296-304 on each row of `logits` (tokens x experts):
@@ -209,6 +210,14 @@ class Oracle:
         self.lib.orc_router_topk(_fptr(a), e, t, e, n_used, 1 if norm_topk else 0, _iptr(idx),
                                  _fptr(wt))
         return idx, wt
+
+    def router_probs(self, x):
+        """(p, the float sum of the numerators) of one row's softmax (forward_cpu.c:165-172)."""
+        a = np.ascontiguousarray(x, dtype=np.float32)
+        p = np.zeros(a.size, dtype=np.float32)
+        sm = np.zeros(1, dtype=np.float32)
+        self.lib.orc_router_probs(_fptr(a), a.size, _fptr(p), _fptr(sm))
+        return p, sm[0]
 
     def pick_rows_diag(self, params, logits, n_rows, n_vocab, hist, seeds, n_threads=1):
         """orc_pick_rows_diag: (ids, diag records (DIAG_DTYPE), seconds)."""

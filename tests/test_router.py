@@ -1,6 +1,9 @@
 """The mixture-of-experts router's choice (forward_cpu.c:165-172, 296-304): the CPU
-restatement pinned by an independent numpy computation and by invariants (CPU), then
-the device kernel behind qs_router_topk against it, bit for bit (GPU)."""
+restatement pinned by an independent numpy computation, by the exact rational sum of the
+host-libm numerators within the float summation bound, by exhaustive tie/NaN/inf
+placements on 1-8 experts against the rule IEEE arithmetic fixes, and by sorting exact
+rationals of the probabilities (CPU); then the device kernel behind qs_router_topk
+against it, bit for bit (GPU)."""
 import numpy as np
 import pytest
 
@@ -68,6 +71,84 @@ def test_oracle_edge_rows(oracle):
     assert list(idx[1]) == [-1] * 4 and (wt[1] == 0).all()
     assert list(idx[2]) == [-1] * 4 and (wt[2] == 0).all()
     assert list(idx[3]) == [-1] * 4 and (wt[3] == 0).all()
+
+
+U24 = 2.0 ** -24
+
+
+@pytest.mark.parametrize("e", [8, 64, 128, 256])
+def test_oracle_sum_within_summation_bound(oracle, e):
+    """The restatement's float sum of the numerators (forward_cpu.c:168-169) lies within the
+    recursive-summation bound of the exact sum of the host-libm numerators expf(x - max):
+    |fl - S| <= (n - 1) u S / (1 - (n - 1) u), u = 2^-24 (a dropped term, a wrong shift or a
+    product in place of a sum fails it); each probability within 3 u of e_i / S, their sum
+    within the bound of 1, and larger logits never less probable."""
+    from fractions import Fraction
+    rng = np.random.default_rng(e)
+    for t in range(40):
+        x = (rng.standard_normal(e) * (3.0 if t % 2 else 0.5)).astype(np.float32)
+        p, sm = oracle.router_probs(x)
+        num = oracle.libm_expf(x - np.float32(x.max()))
+        S = sum(Fraction(float(v)) for v in num)
+        g = (e - 1) * U24 / (1 - (e - 1) * U24)
+        assert abs(Fraction(float(sm)) - S) <= g * S, (t, float(sm), float(S))
+        for i in range(e):
+            exact = Fraction(float(num[i])) / S
+            assert abs(Fraction(float(p[i])) - exact) <= (3 * U24 + 2 * g) * exact, (t, i)
+        tot = sum(Fraction(float(v)) for v in p)
+        assert abs(tot - 1) <= (e + 3) * U24 + 2 * g
+        order = np.argsort(x, kind="stable")
+        assert (np.diff(p[order]) >= 0).all()
+
+
+def _brute_choice(x, n_used):
+    """The rule the reference's scans implement, from IEEE arithmetic rather than its code:
+    a NaN or +inf logit, or a row of -inf, makes the float sum and so every probability NaN
+    (inf - inf, NaN + anything), and no probability beats -1e30: every slot is expert -1;
+    otherwise probabilities order as their logits (expf and the product by one positive
+    normaliser are monotone), the lowest index first among equals, -inf logits last (p 0)."""
+    if any(np.isnan(v) or v == np.inf for v in x) or all(v == -np.inf for v in x):
+        return [-1] * n_used
+    return sorted(range(len(x)), key=lambda i: (-x[i], i))[:n_used]
+
+
+@pytest.mark.parametrize("n,alphabet", [(1, 6), (2, 6), (3, 6), (4, 6), (5, 5), (6, 5),
+                                        (7, 4), (8, 4)])
+def test_oracle_exhaustive_small_rows(oracle, n, alphabet):
+    """Every placement of -inf, -2, 0, 1, NaN and +inf (ties included) over 1-8 experts, for
+    every n_used, against the brute-force rule; weights are 0 exactly for -1 slots and -inf
+    logits, positive otherwise, non-increasing by slot, and with normalisation sum to 1
+    within (n_used + 2) u."""
+    import itertools
+    vals = [-np.inf, 0.0, 1.0, np.nan, -2.0, np.inf][:alphabet]
+    rows_ = np.array(list(itertools.product(vals, repeat=n)), dtype=np.float32)
+    for u in range(1, n + 1):
+        for norm in (0, 1):
+            idx, wt = oracle.router_topk(rows_, u, norm)
+            for r in range(rows_.shape[0]):
+                x = [float(v) for v in rows_[r]]
+                want = _brute_choice(x, u)
+                assert list(idx[r]) == want, (x, u, list(idx[r]), want)
+                w = wt[r]
+                for s, i in enumerate(want):
+                    assert (w[s] == 0) == (i < 0 or x[i] == -np.inf), (x, u, norm, list(w))
+                assert (np.diff(w) <= 0).all(), (x, u, list(w))
+                if norm and w.sum() > 0:
+                    assert abs(float(np.sum(w, dtype=np.float64)) - 1.0) <= (u + 2) * U24
+
+
+@pytest.mark.parametrize("e,u", [(16, 4), (64, 8), (128, 8), (256, 64)])
+def test_oracle_choice_against_rational_sort(oracle, e, u):
+    """The choice equals the n_used first of the probabilities sorted as exact rationals,
+    descending, the lowest index first among equal ones (rows with many float ties)."""
+    from fractions import Fraction
+    rng = np.random.default_rng(100 + e)
+    x = np.round(rng.standard_normal((30, e)) * 2.0, 1).astype(np.float32)
+    idx, _ = oracle.router_topk(x, u, 0)
+    for t in range(x.shape[0]):
+        p, _ = oracle.router_probs(x[t])
+        want = sorted(range(e), key=lambda i: (-Fraction(float(p[i])), i))[:u]
+        assert list(idx[t]) == want, t
 
 
 @pytest.mark.gpu
