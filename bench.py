@@ -41,6 +41,10 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--
        python bench.py --head [--head-rows B]            (the output layer and the pick:
                                                            B x 2048 hidden states, a
                                                            151,936 x 2048 bf16 matrix)
+       python bench.py --head-exact [--head-exact-rows B] (the output layer at the
+                                                           reference's arithmetic, B <= 8
+                                                           rows, a Q6_K 151,936 x 2048
+                                                           matrix, and the pick)
 """
 import argparse
 import json
@@ -85,6 +89,9 @@ def parse():
     ap.add_argument("--head", action="store_true",
                     help="the output layer with the pick (fused) against the layer then a pick")
     ap.add_argument("--head-rows", type=int, default=256)
+    ap.add_argument("--head-exact", action="store_true",
+                    help="the output layer at the reference's arithmetic and the pick")
+    ap.add_argument("--head-exact-rows", type=int, default=1)
     ap.add_argument("--kernel-steps", type=int, default=100,
                     help="picks timed kernel by kernel for the roofline")
     return ap.parse_args()
@@ -314,6 +321,107 @@ def head_bench(args):
         bt.close()
 
 
+def head_exact_bench(args):
+    """The output layer at the reference's arithmetic and the pick: rows/s of
+    qs_batch_pick_head_exact against qs_batch_head_exact_logits followed by qs_batch_pick,
+    and the layer alone, at B (1..8) rows x n_embd 2048 x vocabulary 151,936 with the output
+    matrix in Q6_K (the reference model's type), packed once.  Checked before timing: every
+    logit of the fused call equals the CPU restatement of forward_cpu.c's gemv bit for bit,
+    and the fused ids, generator states and histories equal the unfused pick's and the
+    restatement's sampler on the same logits."""
+    import quasar_amd as qa
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from pyoracle import Oracle
+    B, E, V, WT = args.head_exact_rows, 2048, 151936, qa.WTYPE_Q6_K
+    K, T, TOPP, MINP, RP, LASTN = 40, 0.8, 0.95, 0.05, 1.1, 256
+    rng = np.random.default_rng(12)
+    nb = E // 256
+    wq = rng.integers(0, 256, (V, nb, 210), dtype=np.uint8)
+    dsc = (rng.uniform(0.5, 1.5, (V, nb)) / 2048 / np.sqrt(E)).astype(np.float16)
+    wq[:, :, 208:210] = dsc.view(np.uint8).reshape(V, nb, 2)
+    wq = wq.reshape(V, nb * 210)
+    x = rng.standard_normal((B, E), dtype=np.float32) * np.float32(4.0)
+    hist = rng.integers(0, V, (B, LASTN)).astype(np.int32)
+    seeds = qa.gen_row_seeds(19, 0, B)
+    bats = [qa.Batch(B, V, LASTN) for _ in range(2)]
+    dwr, dx = qa.DeviceBuffer.from_array(wq), qa.DeviceBuffer.from_array(x)
+    w_bytes = qa.head_exact_packed_bytes(WT, E, V)
+    dw = qa.DeviceBuffer(w_bytes)
+    bats[0].head_exact_pack(WT, dwr.ptr, E, V, dw.ptr)
+    bats[0].synchronize()
+    dwr.free()
+    dl, dl2 = qa.DeviceBuffer(4 * B * V), qa.DeviceBuffer(4 * B * V)
+    for bt in bats:
+        bt.config(0, B, T, TOPP, K, MINP, RP, LASTN, seeds=seeds)
+        bt.set_history(0, hist)
+    orc = Oracle()
+    ids_f = bats[0].pick_head_exact(WT, dw.ptr, dx.ptr, E, B, V, dl.ptr)
+    logits = dl.download(np.float32, B * V).reshape(B, V)
+    want = orc.head_gemv(WT, wq, x, V, n_threads=min(16, os.cpu_count() or 1))
+    nan_g, nan_w = np.isnan(logits), np.isnan(want)
+    logit_mism = int(np.count_nonzero(nan_g != nan_w)) + int(np.count_nonzero(
+        logits.view(np.uint32)[~nan_g & ~nan_w] != want.view(np.uint32)[~nan_g & ~nan_w]))
+    dl2.upload(logits)
+    ids_p = bats[1].pick(dl2.ptr, V, B, V)
+    mism = int((ids_f != ids_p).sum())
+    mism += sum(int(bats[0].get_state(r)[0] != bats[1].get_state(r)[0]) for r in range(B))
+    cpu_mism = 0
+    for r in range(B):
+        smp = orc.sampler()
+        smp.config(T, TOPP, K, MINP, RP, LASTN, seed=int(seeds[r]))
+        smp.set_history(hist[r])
+        cpu_mism += int(smp.pick(want[r]) != int(ids_f[r]))
+    # the CPU path: the restatement's gemv of one row on one core and its sampler
+    smp = orc.sampler()
+    t0, n_cpu = time.perf_counter(), 0
+    while n_cpu < 3 or time.perf_counter() - t0 < 6.0:
+        row = orc.head_gemv(WT, wq, x[n_cpu % B][None, :], V, n_threads=1)[0]
+        smp.config(T, TOPP, K, MINP, RP, LASTN, seed=1 + n_cpu)
+        smp.pick(row)
+        n_cpu += 1
+    cpu_rate = n_cpu / (time.perf_counter() - t0)
+    bats[0].time_head_exact(WT, dw.ptr, dx.ptr, E, B, V, dl.ptr, max(args.warmup, 20), 1)
+    res = {}
+    for name, mode in (("fused", 1), ("unfused", 0), ("layer_alone", 2)):
+        bats[0].time_head_exact(WT, dw.ptr, dx.ptr, E, B, V, dl.ptr, 5, mode)
+        res[name] = bats[0].time_head_exact(WT, dw.ptr, dx.ptr, E, B, V, dl.ptr, args.steps,
+                                            mode) * 1e3 / args.steps
+    layer_bytes = w_bytes + 4 * B * E + 4 * B * V
+    us_layer = res["layer_alone"]
+    gbs = layer_bytes / (us_layer * 1e-6) / 1e9
+    # the reference's arithmetic per weight: a byte to float, the scale product, then per row
+    # a product and a sum (2 + 2 B operations), against 256 CUs x 4 SIMDs x 16 lanes at
+    # 2.4 GHz (39.3e12 unpacked lane operations per second: the 157.3 TFLOP/s fp32 peak
+    # counts an FMA as two and packed pairs as two)
+    valu_ops = float(V) * E * (2 + 2 * B)
+    valu_peak = 256 * 4 * 16 * 2.4e9
+    print(json.dumps({
+        "metric": "exact output layer + pick rows/s (fused epilogue)",
+        "value": B / (res["fused"] * 1e-6), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["fused"] / 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"lm_head_exact_b{B}", "rows": B, "n_embd": E, "vocab": V,
+                   "weight_type": "Q6_K", "top_k": K, "temperature": T, "top_p": TOPP,
+                   "min_p": MINP, "repeat_penalty": RP, "last_n": LASTN},
+        "us": {k: round(v, 2) for k, v in res.items()},
+        "roofline": {"kernel": "k_head_exact (layer alone)", "bound": "hbm",
+                     "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "valu_frac": valu_ops / (us_layer * 1e-6) / valu_peak},
+        "cpu_baseline": {"value": cpu_rate, "unit": "rows/s", "cores": 1, "kind": "port",
+                         "sample": f"{n_cpu} rows: the restatement of forward_cpu.c's gemv "
+                                   "(Q6_K rows dequantized, float sums in k order) on one "
+                                   "core, then the restatement of sample.c"},
+        "parity": {"rows": B, "logit_mismatches": logit_mism,
+                   "fused_vs_unfused_mismatches": mism, "fused_vs_cpu_id_mismatches": cpu_mism}
+    }), flush=True)
+    for b_ in (dx, dw, dl, dl2):
+        b_.free()
+    for bt in bats:
+        bt.close()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -327,6 +435,8 @@ def main():
         return router_bench(args)
     if args.head:
         return head_bench(args)
+    if args.head_exact:
+        return head_exact_bench(args)
     import quasar_amd as qa
     from quasar_amd.workloads import BENCH_WORKLOAD, STRESS, WORKLOADS
 

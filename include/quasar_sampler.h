@@ -376,6 +376,60 @@ int qs_batch_time_head(qs_batch *b, const void *d_hidden, const void *d_packed, 
                        int n_rows, int n_vocab, float *d_logits, int32_t *d_out, int iters,
                        int fused, float *ms);
 
+/* ------------------------------------------------------------------------------------
+ * Part 5b: the output layer at the reference's own arithmetic (extension)
+ *
+ * Replaces forward_cpu.c:140-147 (gemv) for the output matrix, forward_cpu.c:321-322:
+ * logits[r][v] = the float sum over k ascending of w[v][k] * xn[r][k], a product then a
+ * sum, with w[v] the GGUF row dequantized exactly as quasar_dequant_row does (quant.c:
+ * F32, F16, Q8_0 and Q6_K rows; Q6_K is the output matrix of the reference's model).  Every
+ * logit equals the reference's bit for bit (NaN payloads aside).  For the few rows a
+ * decoding step produces (the reference decodes one): one thread per vocabulary row keeps
+ * the reference's order, so the cost grows with the rows; larger batches take part 5.
+ * ------------------------------------------------------------------------------------ */
+
+/* GGUF tensor types taken (ggml's type numbers, as gguf.h numbers them). */
+#define QS_WTYPE_F32  0
+#define QS_WTYPE_F16  1
+#define QS_WTYPE_Q8_0 8
+#define QS_WTYPE_Q6_K 14
+#define QS_HEAD_EXACT_MAX_ROWS 8
+#define QS_HEAD_EXACT_MAX_EMBD 16384   /* n_rows * n_embd at most this (64 KB of LDS) */
+
+/* The output matrix is read in an interleaved layout of its own, made once (at model load)
+ * from the n_vocab GGUF rows at d_weight (device memory, the file's bytes: row v at
+ * v * row_bytes): qs_head_exact_packed_bytes bytes at d_packed (16-byte aligned; 0 for a
+ * type or n_embd not taken: F32 and F16 need n_embd a multiple of 16, Q8_0 of 32, Q6_K of
+ * 256), written asynchronously on the batch's stream by qs_batch_head_exact_pack. */
+size_t qs_head_exact_packed_bytes(int wtype, int n_embd, int n_vocab);
+int qs_batch_head_exact_pack(qs_batch *b, int wtype, const void *d_weight, int n_embd,
+                             int n_vocab, void *d_packed);
+
+/* The output layer alone: d_logits[r * n_vocab + v] from d_xn[r * n_embd + k] (fp32),
+ * 1 <= n_rows <= min(max_rows, QS_HEAD_EXACT_MAX_ROWS), n_rows * n_embd at most
+ * QS_HEAD_EXACT_MAX_EMBD, n_vocab a multiple of 4 up to min(max_vocab, 262,144), d_xn and
+ * d_logits 16-byte aligned.  Asynchronous on the batch's stream. */
+int qs_batch_head_exact_logits(qs_batch *b, int wtype, const void *d_packed,
+                               const float *d_xn, int n_embd, int n_rows, int n_vocab,
+                               float *d_logits);
+
+/* The output layer and the pick of rows [0, n_rows) from its logits in one enqueue (the
+ * sampler's first pass taken per tile of 128 logits as they are computed; the decision
+ * reads back only the tiles that hold its candidates): the same ids, generator states and
+ * histories as qs_batch_head_exact_logits followed by qs_batch_pick on d_logits, which it
+ * also writes.  Limits as qs_batch_head_exact_logits. */
+int qs_batch_pick_head_exact(qs_batch *b, int wtype, const void *d_packed, const float *d_xn,
+                             int n_embd, int n_rows, int n_vocab, float *d_logits,
+                             int32_t *d_out, qs_pick_diag *d_diag);
+
+/* `iters` back-to-back calls between two HIP events on the batch's stream: fused = 1,
+ * qs_batch_pick_head_exact; 0, qs_batch_head_exact_logits then qs_batch_pick; 2,
+ * qs_batch_head_exact_logits alone.  Waits; the elapsed milliseconds in *ms (plumbing for
+ * the benchmark). */
+int qs_batch_time_head_exact(qs_batch *b, int wtype, const void *d_packed, const float *d_xn,
+                             int n_embd, int n_rows, int n_vocab, float *d_logits,
+                             int32_t *d_out, int iters, int fused, float *ms);
+
 #ifdef __cplusplus
 }
 #endif

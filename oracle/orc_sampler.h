@@ -110,6 +110,14 @@ void orc_router_topk(const float *logits, long row_stride, int n_tokens, int n_e
 /* One row's softmax (forward_cpu.c:165-172) and the float sum of its numerators. */
 void orc_router_probs(const float *x, int n, float *p, float *sum_out);
 
+/* The output layer (orc_head.c): forward_cpu.c:140-147 over weights of the reference's
+ * GGUF types (ggml numbering) as quant.c dequantizes them. */
+enum { ORC_W_F32 = 0, ORC_W_F16 = 1, ORC_W_Q8_0 = 8, ORC_W_Q6_K = 14 };
+long orc_head_row_bytes(int type, int n);
+void orc_dequant_row(int type, const uint8_t *src, float *dst, int n);
+void orc_head_gemv(int type, const uint8_t *w, const float *x, int nx, int E, int V,
+                   float *y, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -199,6 +199,11 @@ class Oracle:
         lib.orc_router_topk.argtypes = [_F, C.c_long, C.c_int, C.c_int, C.c_int, C.c_int, _I,
                                         _F]
         lib.orc_router_probs.argtypes = [_F, C.c_int, _F, _F]
+        lib.orc_head_row_bytes.argtypes = [C.c_int, C.c_int]
+        lib.orc_head_row_bytes.restype = C.c_long
+        lib.orc_dequant_row.argtypes = [C.c_int, C.c_void_p, _F, C.c_int]
+        lib.orc_head_gemv.argtypes = [C.c_int, C.c_void_p, _F, C.c_int, C.c_int, C.c_int, _F,
+                                      C.c_int]
 
     def router_topk(self, logits, n_used, norm_topk):
         """forward_cpu.c:165-172, 296-304 on each row of `logits` (tokens x experts):
@@ -218,6 +223,26 @@ class Oracle:
         sm = np.zeros(1, dtype=np.float32)
         self.lib.orc_router_probs(_fptr(a), a.size, _fptr(p), _fptr(sm))
         return p, sm[0]
+
+    def head_row_bytes(self, wtype, n):
+        return int(self.lib.orc_head_row_bytes(wtype, n))
+
+    def dequant_row(self, wtype, src, n):
+        """quasar_dequant_row restated (quant.c): n floats from the bytes of one row."""
+        b = np.ascontiguousarray(src, dtype=np.uint8)
+        out = np.zeros(n, dtype=np.float32)
+        self.lib.orc_dequant_row(wtype, b.ctypes.data, _fptr(out), n)
+        return out
+
+    def head_gemv(self, wtype, w_bytes, x, V, n_threads=8):
+        """forward_cpu.c:140-147: logits [nx][V] from V GGUF rows of `wtype` and x [nx][E]."""
+        xb = np.ascontiguousarray(x, dtype=np.float32)
+        nx, E = xb.shape
+        wb = np.ascontiguousarray(w_bytes, dtype=np.uint8)
+        assert wb.size >= V * self.head_row_bytes(wtype, E)
+        y = np.zeros((nx, V), dtype=np.float32)
+        self.lib.orc_head_gemv(wtype, wb.ctypes.data, _fptr(xb), nx, E, V, _fptr(y), n_threads)
+        return y
 
     def pick_rows_diag(self, params, logits, n_rows, n_vocab, hist, seeds, n_threads=1):
         """orc_pick_rows_diag: (ids, diag records (DIAG_DTYPE), seconds)."""
@@ -353,3 +378,28 @@ def parity_report(gpu_ids, gpu_diag, orc_ids, orc_diag):
             "boundary_rows": int(boundary.sum()), "unexplained": int((mism & ~boundary).sum()),
             "inv_outside": int(inv_out), "keep_mismatches": int(keep_mis),
             "paths": {str(k): v for k, v in sorted(paths.items())}}
+
+
+REF_QUANT_SO = os.path.join(os.path.dirname(REF_SO), "libref_quant.so")
+
+
+class RefQuant:
+    """The reference's own quant.c built into oracle/_ref (quasar_dequant_row)."""
+
+    def __init__(self, path=REF_QUANT_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (needs the reference source)")
+        self.lib = C.CDLL(path)
+        self.lib.quasar_dequant_row.argtypes = [C.c_uint32, C.c_void_p, _F, C.c_int]
+        self.lib.q_fp16_to_fp32.argtypes = [C.c_uint16]
+        self.lib.q_fp16_to_fp32.restype = C.c_float
+
+    @staticmethod
+    def available(path=REF_QUANT_SO):
+        return os.path.exists(path)
+
+    def dequant_row(self, wtype, src, n):
+        b = np.ascontiguousarray(src, dtype=np.uint8)
+        out = np.zeros(n, dtype=np.float32)
+        self.lib.quasar_dequant_row(wtype, b.ctypes.data, _fptr(out), n)
+        return out

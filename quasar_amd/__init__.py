@@ -18,9 +18,11 @@ import numpy as np
 
 from . import _native
 from ._native import (MODE_AUTO, MODE_ROW, MODE_SPLIT, MODE_STREAM, PATH_CERT, PATH_EMPTY, PATH_FAST,
-                      PATH_FULL, PATH_GREEDY, QS_EAGAIN, PickDiag, QsError, check, load)
+                      PATH_FULL, PATH_GREEDY, QS_EAGAIN, WTYPE_F16, WTYPE_F32, WTYPE_Q6_K,
+                      WTYPE_Q8_0, PickDiag, QsError, check, load)
 
 __all__ = ["Sampler", "Batch", "DeviceBuffer", "gen_logits_device", "device_info",
+           "head_exact_packed_bytes", "WTYPE_F32", "WTYPE_F16", "WTYPE_Q8_0", "WTYPE_Q6_K",
            "PickDiag", "QsError", "PATH_GREEDY", "PATH_FAST", "PATH_FULL", "PATH_EMPTY",
            "PATH_CERT", "MODE_AUTO", "MODE_SPLIT", "MODE_STREAM", "MODE_ROW", "gen_row_seeds", "gen_history", "QS_EAGAIN"]
 
@@ -114,6 +116,12 @@ def copy_device(dst, src, nbytes, iters=1):
 def head_packed_bytes(n_embd, n_vocab):
     """Bytes of the packed output matrix (qs_head_packed_bytes; 0 for sizes not taken)."""
     return int(load().qs_head_packed_bytes(n_embd, n_vocab))
+
+
+def head_exact_packed_bytes(wtype, n_embd, n_vocab):
+    """Bytes of the exact output layer's packed matrix (qs_head_exact_packed_bytes; 0 for a
+    type or size not taken)."""
+    return int(load().qs_head_exact_packed_bytes(wtype, n_embd, n_vocab))
 
 
 def device_info():
@@ -312,6 +320,47 @@ class Batch:
                                            n_vocab, logits_ptr, self._out.ptr, iters,
                                            int(fused), C.byref(ms)),
               "qs_batch_time_head")
+        return ms.value
+
+    def head_exact_pack(self, wtype, weight_ptr, n_embd, n_vocab, packed_ptr):
+        """The GGUF output matrix (rows of type wtype) into the exact output layer's layout
+        (qs_batch_head_exact_pack), asynchronous; packed_ptr holds
+        head_exact_packed_bytes(wtype, n_embd, n_vocab) bytes."""
+        check(self._lib.qs_batch_head_exact_pack(self._b, wtype, weight_ptr, n_embd, n_vocab,
+                                                 packed_ptr), "qs_batch_head_exact_pack")
+
+    def head_exact_logits(self, wtype, packed_ptr, xn_ptr, n_embd, n_rows, n_vocab,
+                          logits_ptr):
+        """The output layer at the reference's arithmetic alone (qs_batch_head_exact_logits),
+        asynchronous."""
+        check(self._lib.qs_batch_head_exact_logits(self._b, wtype, packed_ptr, xn_ptr, n_embd,
+                                                   n_rows, n_vocab, logits_ptr),
+              "qs_batch_head_exact_logits")
+
+    def pick_head_exact(self, wtype, packed_ptr, xn_ptr, n_embd, n_rows, n_vocab, logits_ptr,
+                        diag=False):
+        """That output layer and the pick of rows [0, n_rows) (qs_batch_pick_head_exact);
+        returns ids (and a list of PickDiag when diag)."""
+        check(self._lib.qs_batch_pick_head_exact(self._b, wtype, packed_ptr, xn_ptr, n_embd,
+                                                 n_rows, n_vocab, logits_ptr, self._out.ptr,
+                                                 self._diag.ptr if diag else None),
+              "qs_batch_pick_head_exact")
+        self.synchronize()
+        ids = self._out.download(np.int32, n_rows)
+        if not diag:
+            return ids
+        raw = self._diag.download(np.uint8, C.sizeof(PickDiag) * n_rows)
+        return ids, list((PickDiag * n_rows).from_buffer_copy(raw.tobytes()))
+
+    def time_head_exact(self, wtype, packed_ptr, xn_ptr, n_embd, n_rows, n_vocab, logits_ptr,
+                        iters, fused):
+        """Milliseconds of `iters` calls (qs_batch_time_head_exact): fused picks (1), the
+        layer then a pick (0), the layer alone (2)."""
+        ms = C.c_float(0)
+        check(self._lib.qs_batch_time_head_exact(self._b, wtype, packed_ptr, xn_ptr, n_embd,
+                                                 n_rows, n_vocab, logits_ptr, self._out.ptr,
+                                                 iters, int(fused), C.byref(ms)),
+              "qs_batch_time_head_exact")
         return ms.value
 
     def time_picks(self, logits_ptrs, row_stride, n_rows, n_vocab, iters):

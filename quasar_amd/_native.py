@@ -14,6 +14,8 @@ QS_EINVAL, QS_ENOMEM, QS_EDEVICE = -22, -12, -5
 QS_EAGAIN = -11
 PATH_GREEDY, PATH_FAST, PATH_FULL, PATH_EMPTY, PATH_CERT = 0, 1, 2, 3, 4
 MODE_AUTO, MODE_SPLIT, MODE_STREAM, MODE_ROW = 0, 1, 2, 3
+WTYPE_F32, WTYPE_F16, WTYPE_Q8_0, WTYPE_Q6_K = 0, 1, 8, 14   # GGUF tensor types
+HEAD_EXACT_MAX_ROWS, HEAD_EXACT_MAX_EMBD = 8, 16384
 
 
 class PickDiag(C.Structure):
@@ -79,6 +81,12 @@ PROTOS = [
     ("qs_batch_pick_head", _i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     ("qs_batch_time_head", _i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _i, _i,
                                 C.POINTER(C.c_float)]),
+    ("qs_head_exact_packed_bytes", _sz, [_i, _i, _i]),
+    ("qs_batch_head_exact_pack", _i, [_vp, _i, _vp, _i, _i, _vp]),
+    ("qs_batch_head_exact_logits", _i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp]),
+    ("qs_batch_pick_head_exact", _i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    ("qs_batch_time_head_exact", _i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp, _vp, _i, _i,
+                                      C.POINTER(C.c_float)]),
 ]
 
 _lib = None

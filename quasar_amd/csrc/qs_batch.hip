@@ -952,6 +952,8 @@ int qs_batch_set_spin_limit(qs_batch *b, int attempts) {
 
 // The output layer's arguments, checked; allocates its records and history bitmap on the
 // first call (zeroed once: each pick leaves the bitmap zero).
+static int head_records(qs_batch *b, int n_rows);
+
 static int head_check(qs_batch *b, const void *d_hidden, const void *d_weight, int n_embd,
                       int n_rows, int n_vocab, const float *d_logits, bool pick) {
     if (!b || !d_hidden || !d_weight || !d_logits) {
@@ -969,6 +971,14 @@ static int head_check(qs_batch *b, const void *d_hidden, const void *d_weight, i
         return QS_EINVAL;
     }
     if (!pick) return 0;
+    return head_records(b, n_rows);
+}
+
+// A fused pick's tile records and history bitmap: allocated on the first such pick (for
+// min(max_rows, 256) rows and the batch's vocabulary; the bitmap zeroed once, each pick
+// leaving it zero) or cleared after a failed one; then the rows' parameters checked.
+static int head_records(qs_batch *b, int n_rows) {
+    const int rmax = b->max_rows < QS_HEAD_MAX_ROWS ? b->max_rows : QS_HEAD_MAX_ROWS;
     if (!b->d_hrec) {
         const size_t nt = (size_t)(b->max_vocab + QS_HEAD_TILE - 1) / QS_HEAD_TILE;
         int rc = dev_alloc(&b->d_hrec, (size_t)rmax * nt, "output layer records");
@@ -1060,6 +1070,103 @@ int qs_batch_time_head(qs_batch *b, const void *d_hidden, const void *d_weight, 
         } else {
             rc = qs_batch_head_logits(b, d_hidden, d_weight, n_embd, n_rows, n_vocab, d_logits);
             if (!rc) rc = qs_batch_pick(b, d_logits, n_vocab, n_rows, n_vocab, d_out, nullptr);
+        }
+        if (rc) return rc;
+    }
+    HIP_TRY(hipEventRecord(b->ev1, b->stream), "event");
+    HIP_TRY(hipEventSynchronize(b->ev1), "event sync");
+    HIP_TRY(hipEventElapsedTime(ms, b->ev0, b->ev1), "elapsed");
+    return 0;
+}
+
+// The exact output layer's arguments, checked (with `pick`, its records as head_check).
+static int head_exact_check(qs_batch *b, int wtype, const void *d_packed, const float *d_xn,
+                            int n_embd, int n_rows, int n_vocab, const float *d_logits,
+                            bool pick) {
+    if (!b || !d_packed || !d_xn || !d_logits) {
+        qs_set_error("exact output layer: null argument");
+        return QS_EINVAL;
+    }
+    const int rmax = b->max_rows < QS_HEAD_EXACT_MAX_ROWS ? b->max_rows : QS_HEAD_EXACT_MAX_ROWS;
+    const int vmax = b->max_vocab < QS_HEAD_MAX_VOCAB ? b->max_vocab : QS_HEAD_MAX_VOCAB;
+    if (!qs_head_exact_shape_ok(wtype, n_embd) || n_rows < 1 || n_rows > rmax ||
+        (int64_t)n_rows * n_embd > QS_HEAD_EXACT_MAX_EMBD || n_vocab < 4 || n_vocab > vmax ||
+        n_vocab % 4 != 0 || (uintptr_t)d_packed % 16 != 0 || (uintptr_t)d_xn % 16 != 0 ||
+        (uintptr_t)d_logits % 16 != 0) {
+        qs_set_error("exact output layer: type %d with embedding %d (F32/F16: a multiple of 16, "
+                     "Q8_0: 32, Q6_K: 256), rows %d (1..%d, rows x embedding at most %d), "
+                     "vocab %d (a multiple of 4 up to %d), 16-byte aligned buffers", wtype,
+                     n_embd, n_rows, rmax, QS_HEAD_EXACT_MAX_EMBD, n_vocab, vmax);
+        return QS_EINVAL;
+    }
+    return pick ? head_records(b, n_rows) : 0;
+}
+
+size_t qs_head_exact_packed_bytes(int wtype, int n_embd, int n_vocab) {
+    if (n_vocab > QS_HEAD_MAX_VOCAB) return 0;
+    return qs_head_exact_bytes(wtype, n_embd, n_vocab);
+}
+
+int qs_batch_head_exact_pack(qs_batch *b, int wtype, const void *d_weight, int n_embd,
+                             int n_vocab, void *d_packed) {
+    if (!b || !d_weight || !d_packed || !qs_head_exact_packed_bytes(wtype, n_embd, n_vocab) ||
+        (uintptr_t)d_packed % 16 != 0) {
+        qs_set_error("qs_batch_head_exact_pack: type %d, embedding %d, vocab %d (up to %d), "
+                     "non-null buffers, the packed one 16-byte aligned", wtype, n_embd, n_vocab,
+                     QS_HEAD_MAX_VOCAB);
+        return QS_EINVAL;
+    }
+    return qs_head_exact_pack_launch(d_weight, wtype, n_embd, n_vocab, d_packed, b->stream);
+}
+
+int qs_batch_head_exact_logits(qs_batch *b, int wtype, const void *d_packed,
+                               const float *d_xn, int n_embd, int n_rows, int n_vocab,
+                               float *d_logits) {
+    if (const int rc = head_exact_check(b, wtype, d_packed, d_xn, n_embd, n_rows, n_vocab,
+                                        d_logits, false))
+        return rc;
+    RowState st{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
+                b->max_last_n > 0 ? b->max_last_n : 1};
+    return qs_head_exact_launch(d_packed, wtype, d_xn, n_embd, n_rows, n_vocab, d_logits, st,
+                                nullptr, nullptr, b->stream);
+}
+
+int qs_batch_pick_head_exact(qs_batch *b, int wtype, const void *d_packed, const float *d_xn,
+                             int n_embd, int n_rows, int n_vocab, float *d_logits,
+                             int32_t *d_out, qs_pick_diag *d_diag) {
+    if (!d_out) { qs_set_error("qs_batch_pick_head_exact: null output"); return QS_EINVAL; }
+    if (const int rc = head_exact_check(b, wtype, d_packed, d_xn, n_embd, n_rows, n_vocab,
+                                        d_logits, true))
+        return rc;
+    RowState st{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
+                b->max_last_n > 0 ? b->max_last_n : 1};
+    int rc = qs_head_prep_launch(n_rows, n_vocab, st, b->d_hbits, b->stream);
+    if (!rc)
+        rc = qs_head_exact_launch(d_packed, wtype, d_xn, n_embd, n_rows, n_vocab, d_logits, st,
+                                  b->d_hrec, b->d_hbits, b->stream);
+    if (rc) {
+        b->hbits_dirty = true;           // the bitmap kernel may have run
+        return rc;
+    }
+    return qs_head_decide_launch(d_logits, n_rows, n_vocab, st, b->sc, b->d_hrec, d_out, d_diag,
+                                 b->stream);
+}
+
+int qs_batch_time_head_exact(qs_batch *b, int wtype, const void *d_packed, const float *d_xn,
+                             int n_embd, int n_rows, int n_vocab, float *d_logits,
+                             int32_t *d_out, int iters, int fused, float *ms) {
+    if (!b || iters < 1 || !ms || fused < 0 || fused > 2) return QS_EINVAL;
+    HIP_TRY(hipEventRecord(b->ev0, b->stream), "event");
+    for (int i = 0; i < iters; ++i) {
+        int rc;
+        if (fused == 1) {
+            rc = qs_batch_pick_head_exact(b, wtype, d_packed, d_xn, n_embd, n_rows, n_vocab,
+                                          d_logits, d_out, nullptr);
+        } else {
+            rc = qs_batch_head_exact_logits(b, wtype, d_packed, d_xn, n_embd, n_rows, n_vocab,
+                                            d_logits);
+            if (!rc && fused == 0)
+                rc = qs_batch_pick(b, d_logits, n_vocab, n_rows, n_vocab, d_out, nullptr);
         }
         if (rc) return rc;
     }

@@ -644,6 +644,56 @@ int qs_head_pack_launch(const void *d_weight, int n_embd, int n_vocab, void *d_p
     return 0;
 }
 
+int qs_head_prep_launch(int n_rows, int n_vocab, const RowState &st, uint32_t *hbits,
+                        hipStream_t stream) {
+    HeadArgs a;
+    memset(&a, 0, sizeof a);
+    a.n_rows = n_rows;
+    a.V = n_vocab;
+    a.hb = hbits;
+    a.st = st;
+    hipLaunchKernelGGL(k_head_prep, dim3((unsigned)n_rows), dim3(256), 0, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        qs_set_error("output layer history bitmap launch: %s", hipGetErrorString(e));
+        return QS_EDEVICE;
+    }
+    return 0;
+}
+
+int qs_head_decide_launch(float *d_logits, int n_rows, int n_vocab, const RowState &st,
+                          const Scratch &sc, HeadRec *rec, int32_t *out, qs_pick_diag *diag,
+                          hipStream_t stream) {
+    HeadArgs a;
+    memset(&a, 0, sizeof a);
+    a.n_rows = n_rows;
+    a.V = n_vocab;
+    a.ntiles = (n_vocab + HT - 1) / HT;
+    a.logits = d_logits;
+    a.rec = rec;
+    a.records = 1;
+    a.st = st;
+    PartArgs pa;
+    pa.logits = d_logits;
+    pa.stride = n_vocab;
+    pa.vocab = n_vocab;
+    pa.n_rows = n_rows;
+    pa.parts = 1;
+    pa.part_len = n_vocab;
+    pa.xcd_map = 0;
+    pa.st = st;
+    pa.sc = sc;
+    pa.out = out;
+    pa.diag = diag;
+    hipLaunchKernelGGL(k_head_decide, dim3((unsigned)n_rows), dim3(ND), 0, stream, a, pa);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        qs_set_error("output layer decision launch: %s", hipGetErrorString(e));
+        return QS_EDEVICE;
+    }
+    return 0;
+}
+
 int qs_head_launch(const void *d_hidden, const void *d_weight, int n_embd, int n_rows,
                    int n_vocab, float *d_logits, const RowState &st, const Scratch &sc,
                    HeadRec *rec, uint32_t *hbits, int32_t *out, qs_pick_diag *diag,

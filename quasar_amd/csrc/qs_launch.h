@@ -71,6 +71,31 @@ struct HeadRec {
     double sum, term;
 };
 
+// The history bitmap of the pick's rows (hbits zero before; the output layer's epilogue
+// clears the bits it reads), and the row decisions from the tile records and the written
+// logits: shared by both output layers.
+int qs_head_prep_launch(int n_rows, int n_vocab, const qs::RowState &st, uint32_t *hbits,
+                        hipStream_t stream);
+int qs_head_decide_launch(float *d_logits, int n_rows, int n_vocab, const qs::RowState &st,
+                          const qs::Scratch &sc, HeadRec *rec, int32_t *out, qs_pick_diag *diag,
+                          hipStream_t stream);
+
+// ---- the output layer at the reference's arithmetic (qs_head_exact.hip) ----
+
+// Whether the exact layer takes this weight type and embedding size; the packed matrix's
+// bytes (0: not taken).
+int qs_head_exact_shape_ok(int wtype, int n_embd);
+size_t qs_head_exact_bytes(int wtype, int n_embd, int n_vocab);
+// Enqueue: the GGUF rows at d_weight (n_vocab rows of wtype) into the packed layout.
+int qs_head_exact_pack_launch(const void *d_weight, int wtype, int n_embd, int n_vocab,
+                              void *d_packed, hipStream_t stream);
+// Enqueue: d_logits[n_rows][n_vocab] from the packed matrix and d_xn[n_rows][n_embd]
+// (n_rows <= QS_HEAD_EXACT_MAX_ROWS); with rec, also the tile records for
+// qs_head_decide_launch (hbits set by qs_head_prep_launch, left zero).
+int qs_head_exact_launch(const void *d_packed, int wtype, const float *d_xn, int n_embd,
+                         int n_rows, int n_vocab, float *d_logits, const qs::RowState &st,
+                         HeadRec *rec, uint32_t *hbits, hipStream_t stream);
+
 // Elements of the packed output matrix (the vocabulary rounded up to whole tiles).
 size_t qs_head_packed_elems(int n_embd, int n_vocab);
 // Enqueue on `stream`: the bf16 [n_vocab][n_embd] output matrix into the tile order the
