@@ -1128,7 +1128,7 @@ int qs_batch_head_exact_logits(qs_batch *b, int wtype, const void *d_packed,
     RowState st{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
                 b->max_last_n > 0 ? b->max_last_n : 1};
     return qs_head_exact_launch(d_packed, wtype, d_xn, n_embd, n_rows, n_vocab, d_logits, st,
-                                nullptr, nullptr, b->stream);
+                                nullptr, b->stream);
 }
 
 int qs_batch_pick_head_exact(qs_batch *b, int wtype, const void *d_packed, const float *d_xn,
@@ -1140,14 +1140,9 @@ int qs_batch_pick_head_exact(qs_batch *b, int wtype, const void *d_packed, const
         return rc;
     RowState st{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
                 b->max_last_n > 0 ? b->max_last_n : 1};
-    int rc = qs_head_prep_launch(n_rows, n_vocab, st, b->d_hbits, b->stream);
-    if (!rc)
-        rc = qs_head_exact_launch(d_packed, wtype, d_xn, n_embd, n_rows, n_vocab, d_logits, st,
-                                  b->d_hrec, b->d_hbits, b->stream);
-    if (rc) {
-        b->hbits_dirty = true;           // the bitmap kernel may have run
-        return rc;
-    }
+    const int rc = qs_head_exact_launch(d_packed, wtype, d_xn, n_embd, n_rows, n_vocab,
+                                        d_logits, st, b->d_hrec, b->stream);
+    if (rc) return rc;
     return qs_head_decide_launch(d_logits, n_rows, n_vocab, st, b->sc, b->d_hrec, d_out, d_diag,
                                  b->stream);
 }

@@ -40,6 +40,7 @@
 #include <cfloat>
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 #include <cstring>
 
 #include "../../include/quasar_sampler.h"
@@ -402,13 +403,19 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
     if (tid < QS_EXPF_TAB_N) dl.dl.tab[tid] = c_tab_head[tid];
     RowHist hist{0ull, 0, 0};
     if (tid < 64 && !greedy) hist = row_hist(st, row);
-    // the row's max from the tile records
+    // the row's tile records (each thread's RPT of them kept in registers) and its max
+    constexpr int RPT = (TMAX + ND - 1) / ND;
+    HeadRec hr[RPT];
     uint32_t mk = 0u;
-    for (int t = tid; t < NT_; t += ND) {
-        const uint32_t k = rr[t].maxk;
-        HL.tmax[t] = k;
-        HL.sel[t] = -1;
-        mk = max(mk, k);
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int t = tid + k * ND;
+        if (t < NT_) {
+            hr[k] = rr[t];
+            HL.tmax[t] = hr[k].maxk;
+            HL.sel[t] = -1;
+            mk = max(mk, hr[k].maxk);
+        }
     }
     // the first ND history ids, requested with the records
     const float rp = P.repeat_penalty;
@@ -453,8 +460,11 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
         // tile lies wholly in or out of the window
         double lo = 0.0, hi = 0.0;
         int nin = 0, unk = 0;
-        for (int t = tid; t < NT_; t += ND) {
-            const HeadRec h = rr[t];
+#pragma unroll
+        for (int k = 0; k < RPT; ++k) {
+            const int t = tid + k * ND;
+            if (t >= NT_) continue;
+            const HeadRec &h = hr[k];
             const float maxw = key2f(h.maxk);
             const CertPart cp = cert_part_c(maxw, h.c, h.sum, h.term, inv_t, msc, thr);
             lo += cp.lo;
@@ -470,12 +480,12 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
         nin = wave_sum_i(nin);
         unk = __ballot(unk != 0) != 0ull;
         if (lane == 0) { HL.plo[wv] = lo; HL.phi[wv] = hi; HL.pin[wv] = nin; HL.pkn[wv] = unk; }
-        __syncthreads();
         if (kp <= 64) {
             // a bound at or below the kp-th largest tile maximum from one wavefront: the
             // kp-th largest of its lanes' maxima (a subset of the tile maxima), so at least
             // kp tiles lie at or above it; a few more tiles are read than with the exact
-            // kp-th, without the block's radix select
+            // kp-th, without the block's radix select (the maxima were stored before the
+            // last barrier)
             if (wv == 0) {
                 uint32_t lm = 0u;
                 for (int t = lane; t < NT_; t += 64) lm = max(lm, HL.tmax[t]);
@@ -486,6 +496,7 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
             __syncthreads();
             th = HL.th;
         } else {
+            __syncthreads();
             th = block_kth<ND>(HL.tmax, NT_, kp, dl.dl.hist, dl.dl.sh + 4);
         }
         if (tid == 0) {
@@ -540,66 +551,92 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
         }
         __syncthreads();
     }
-    // the selected tiles' penalised logits, two tiles per wavefront (one per half) and 4
-    // logits a lane, GU tile pairs' loads issued together: a greedy row's first max; a
-    // sampled row's logits at or above th as candidates (NaN never), the others raising the
-    // rejected bound
+    // the selected tiles' penalised logits, GR float4s a thread in flight (a flat index over
+    // (slot, float4 of the tile): 32 lanes a tile, one round trip for up to ND * GR / 32
+    // tiles): a greedy row's first max; a sampled row's logits at or above th as candidates
+    // (NaN never), the others raising the rejected bound
     static_assert(HT == 128, "a tile is 32 lanes x 4 logits");
-    constexpr int GU = 4;
-    const int half = lane >> 5, hl = lane & 31;
+    constexpr int QT = HT / 4, GR = 16;
+    const int nq = nsel * QT;
+    const float thf = key2f(th);
+    if (!greedy) myrej = max(myrej, th - 1u);            // (th > KEY_NEG_INF: a key below it)
     float bv = -INFINITY;
     int bi = -1;
-    for (int s0 = wv * 2 * GU; s0 < nsel; s0 += ND / 64 * 2 * GU) {
-        float4 vv[GU];
+    // rounds of GR float4s a thread, loaded together; a sampled row looks only at the
+    // float4s reaching th (the penalty only lowers a logit, a float below thf has a key below
+    // th, and with a NaN the test fails and the float4 is looked at): what it leaves is
+    // bounded by th - 1, the rejected bound taken above
+    auto gather = [&](auto greedy_c) {
+        constexpr bool G = decltype(greedy_c)::value;
+        for (int base = 0; base < nq; base += ND * GR) {
+            float4 vv[GR];
+            uint32_t tk[GR], kv[GR][4];                   // candidates taken, their keys
 #pragma unroll
-        for (int u = 0; u < GU; ++u) {
-            vv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-            const int s = s0 + 2 * u + half;
-            if (s < nsel) {
-                const int c = HL.stile[s] * HT + hl * 4;
-                if (c < V) vv[u] = *(const float4 *)(x + c);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < GU; ++u) {
-            if (s0 + 2 * u >= nsel) break;               // (uniform)
-            const int s = s0 + 2 * u + half;
-            const bool ok = s < nsel;
-            const int c = ok ? HL.stile[s] * HT + hl * 4 : V;
-            float w[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
-            const uint32_t bits = ok ? HL.selbits[s][hl >> 3] >> ((hl * 4) & 31) : 0u;
-            bool take[4];
-            uint32_t key[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool in = c + e < V;
-                if (in && ((bits >> e) & 1u)) w[e] = penalise_r(w[e], rp, rinv);
-                if (greedy) {
-                    if (in && w[e] == w[e]) best_combine(bv, bi, w[e], c + e);
-                    take[e] = false;
-                    key[e] = 0u;
-                    continue;
-                }
-                key[e] = f2key(w[e]);
-                take[e] = in && w[e] == w[e] && key[e] >= th;
-                if (in && w[e] == w[e] && !take[e]) myrej = max(myrej, key[e]);
-            }
-            if (greedy) continue;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint64_t m = __ballot(take[e]);
-                if (!m) continue;
-                int base = 0;
-                if (lane == 0) base = atomicAdd(&dl.dl.sh[3], __popcll(m));
-                base = __shfl(base, 0, 64);
-                const int pos = base + lane_prefix(m);
-                if (take[e] && pos < FCAP) {
-                    dl.keys[pos] = key[e];
-                    dl.ids[pos] = c + e;
+            for (int u = 0; u < GR; ++u) {
+                tk[u] = 0u;
+                vv[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+                const int i = base + u * ND + tid;
+                if (i < nq) {
+                    const int c = HL.stile[i / QT] * HT + (i % QT) * 4;
+                    if (c < V) vv[u] = *(const float4 *)(x + c);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < GR; ++u) {
+                if (base + u * ND >= nq) break;           // (uniform)
+                if (!G && !__ballot(!(max4(vv[u]) < thf))) continue;
+                const int i = base + u * ND + tid, sl = i / QT, q = i % QT;
+                const bool ok = i < nq;
+                const int c = ok ? HL.stile[sl] * HT + q * 4 : V;
+                float w[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+                const uint32_t bits = ok ? (HL.selbits[sl][q >> 3] >> ((q * 4) & 31)) & 0xFu : 0u;
+                if (__ballot(bits != 0u)) {               // (ids past V are never marked)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if ((bits >> e) & 1u) w[e] = penalise_r(w[e], rp, rinv);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool live = c + e < V && w[e] == w[e];
+                    if constexpr (G) {
+                        if (live) best_combine(bv, bi, w[e], c + e);
+                    } else {
+                        kv[u][e] = f2key(w[e]);
+                        tk[u] |= (live && kv[u][e] >= th ? 1u : 0u) << e;
+                    }
+                }
+            }
+            if constexpr (!G) {
+                // this thread's candidates at consecutive positions: one LDS atomic a
+                // wavefront
+                int cnt = 0;
+#pragma unroll
+                for (int u = 0; u < GR; ++u) cnt += __builtin_popcount(tk[u]);
+                const int incl = wave_scan(cnt);
+                const int wtot = __builtin_amdgcn_readlane(incl, 63);
+                if (wtot == 0) continue;                  // (uniform)
+                int at = 0;
+                if (lane == 63) at = atomicAdd(&dl.dl.sh[3], wtot);
+                int pos = __shfl(at, 63, 64) + incl - cnt;
+#pragma unroll
+                for (int u = 0; u < GR; ++u) {
+                    if (!tk[u]) continue;
+                    const int i = base + u * ND + tid;
+                    const int c = HL.stile[i / QT] * HT + (i % QT) * 4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (((tk[u] >> e) & 1u) && pos < FCAP) {
+                            dl.keys[pos] = kv[u][e];
+                            dl.ids[pos] = c + e;
+                        }
+                        pos += (tk[u] >> e) & 1u;
+                    }
+                }
+            }
         }
-    }
+    };
+    if (greedy) gather(std::true_type{});
+    else gather(std::false_type{});
     if (greedy) {
         block_best(bv, bi, dl);
         if (tid == 0) record_greedy(row, P, bv, bi, maxl, x[0], st, pa.out, pa.diag);
@@ -615,10 +652,23 @@ __global__ void __launch_bounds__(ND) k_head_decide(HeadArgs a, PartArgs pa) {
     __syncthreads();
     if (tid == 0) dl.ct = t;
     int status;
-    if (!(isfinite(msc) && fabsf(msc) < CERT_MSC_MAX)) status = CF_MSC;
-    else status = cert_row_block<ND>(row, P, t, dl.keys, dl.ids, dl.srt, dl.dl, st, pa.out,
-                                     pa.diag, hist);
+    if (!(isfinite(msc) && fabsf(msc) < CERT_MSC_MAX)) {
+        status = CF_MSC;
+    } else if (K <= 64 && t.total <= WAVE_CAND) {
+        // one wavefront decides (the row kernel's decision); the others take its status
+        if (wv == 0) {
+            const int s0 = cert_row_wave(row, P, t, dl.keys, dl.ids, dl.srt, dl.dl.tab, st,
+                                         pa.out, pa.diag, hist);
+            if (lane == 0) dl.dl.sh[7] = s0;
+        }
+        __syncthreads();
+        status = dl.dl.sh[7];
+    } else {
+        status = cert_row_block<ND>(row, P, t, dl.keys, dl.ids, dl.srt, dl.dl, st, pa.out,
+                                    pa.diag, hist);
+    }
     if (status == 0) return;
+    __syncthreads();
     exact_row(pa, row, P, t, dl, hist, status);
 }
 

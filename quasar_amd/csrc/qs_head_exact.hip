@@ -14,8 +14,8 @@
 // k_head_exact<type, rows>, 256 threads (256 vocabulary rows, two tiles of 128): the pick's
 // hidden rows copied into LDS, the loop over the row's blocks in k order (four elements of a
 // hidden row per broadcast read), then the logits written; with records (the fused
-// pick), per (hidden row, tile of 128): the repeat penalty from the history bits k_head_prep
-// set (cleared here), the penalised max and min keys, the NaN count and the certified sums
+// pick), per (hidden row, tile of 128): the repeat penalty (the rows' history ids marked in
+// LDS by each workgroup for its vocabulary rows), the penalised max and min keys, the NaN count and the certified sums
 // against an integer exponent base, exactly what the other output layer's epilogue
 // records, so the same decision kernel (k_head_decide) finishes the pick.
 
@@ -114,7 +114,6 @@ struct ExactArgs {
     const float *x;                     // [n_rows][E] hidden rows (xn)
     int E, V, n_rows, ntiles, ua, nd;
     float *logits;                      // [n_rows][V]
-    uint32_t *hb;                       // history bits: bit b of word v (fused pick)
     HeadRec *rec;                       // [n_rows][ntiles]; null: the logits only
     RowState st;
 };
@@ -261,8 +260,28 @@ __global__ void __launch_bounds__(XNT) k_head_exact(ExactArgs a) {
     const int r = blockIdx.x * XNT + tid;          // this thread's vocabulary row
     const int g = blockIdx.x * (XNT / 64) + wv;    // its group of 64 in the packed layout
     extern __shared__ float4 xs4[];                // the pick's hidden rows, n_rows x E
+    __shared__ uint32_t s_hb[XNT];                 // bit b: the row in row b's history
     for (int i = tid; i < a.n_rows * a.E / 4; i += XNT) xs4[i] = ((const float4 *)a.x)[i];
+    s_hb[tid] = 0u;
     __syncthreads();
+    if (a.rec) {
+        // sample.c:118-120: the history ids of each pick row that fall in this workgroup's
+        // vocabulary rows (duplicates set the same bit); read by the records below
+        const int r0 = blockIdx.x * XNT;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const qs_row_param P = row_param(a.st, b);
+            const int cap = P.ring_cap;
+            int len, head;
+            ring_pos(a.st, b, cap, len, head);
+            if (!(P.repeat_penalty > 1.0f) || len <= 0 || cap <= 0) continue;
+            const int32_t *ring = a.st.ring + (int64_t)b * a.st.ring_stride;
+            for (int j = tid; j < len; j += XNT) {
+                const int id = ring[qs_ring_slot(cap, head, j)];
+                if (id >= r0 && id < r0 + XNT && id < a.V) atomicOr(&s_hb[id - r0], 1u << b);
+            }
+        }
+    }
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
@@ -282,8 +301,7 @@ __global__ void __launch_bounds__(XNT) k_head_exact(ExactArgs a) {
     auto &s_nan = ep.nan;
     auto &s_s = ep.s;
     auto &s_t = ep.t;
-    const uint32_t hw = r < V ? a.hb[r] : 0u;      // bit b: id r in row b's history
-    if (hw) a.hb[r] = 0u;
+    const uint32_t hw = s_hb[tid];                 // bit b: id r in row b's history
     float w[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -407,7 +425,7 @@ int qs_head_exact_pack_launch(const void *d_weight, int wtype, int n_embd, int n
 
 int qs_head_exact_launch(const void *d_packed, int wtype, const float *d_xn, int n_embd,
                          int n_rows, int n_vocab, float *d_logits, const RowState &st,
-                         HeadRec *rec, uint32_t *hbits, hipStream_t stream) {
+                         HeadRec *rec, hipStream_t stream) {
     const XFmt f = xfmt(wtype, n_embd);
     const int groups = (n_vocab + 63) / 64;
     ExactArgs a;
@@ -421,7 +439,6 @@ int qs_head_exact_launch(const void *d_packed, int wtype, const float *d_xn, int
     a.ua = f.ua;
     a.nd = f.nd;
     a.logits = d_logits;
-    a.hb = hbits;
     a.rec = rec;
     a.st = st;
     hipError_t e;

@@ -91,10 +91,10 @@ int qs_head_exact_pack_launch(const void *d_weight, int wtype, int n_embd, int n
                               void *d_packed, hipStream_t stream);
 // Enqueue: d_logits[n_rows][n_vocab] from the packed matrix and d_xn[n_rows][n_embd]
 // (n_rows <= QS_HEAD_EXACT_MAX_ROWS); with rec, also the tile records for
-// qs_head_decide_launch (hbits set by qs_head_prep_launch, left zero).
+// qs_head_decide_launch (the repeat penalty from the rows' rings, read by each workgroup).
 int qs_head_exact_launch(const void *d_packed, int wtype, const float *d_xn, int n_embd,
                          int n_rows, int n_vocab, float *d_logits, const qs::RowState &st,
-                         HeadRec *rec, uint32_t *hbits, hipStream_t stream);
+                         HeadRec *rec, hipStream_t stream);
 
 // Elements of the packed output matrix (the vocabulary rounded up to whole tiles).
 size_t qs_head_packed_elems(int n_embd, int n_vocab);
