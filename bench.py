@@ -34,7 +34,8 @@ Also reported on the same JSON line:
                 restatement on every row: id mismatches, draws within 1e-6 of a CDF
                 boundary, mismatches not explained by one, normalisers outside the GPU's
                 (proven) value or interval, kept-prefix mismatches
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--mode M]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--rows B]
+                       [--mode M]
        python bench.py --calibrate-copy [--copy-mib N]   (copies of N MiB, for the counters)
        python bench.py --router [--router-tokens T]      (the MoE router's expert choice:
                                                            T tokens x 128 experts, top 8)
@@ -68,6 +69,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default=None)
+    ap.add_argument("--rows", type=int, default=0,
+                    help="the workload's settings at this batch size (0: its own)")
     ap.add_argument("--settle-s", type=float, default=0.25,
                     help="untimed picks for this long before the warm-up steps: the GPU "
                          "leaves the idle clocks of input generation (0: none)")
@@ -442,6 +445,10 @@ def main():
 
     allw = dict(WORKLOADS, **STRESS)
     w = allw[args.workload or BENCH_WORKLOAD]
+    wname = w.name
+    if args.rows > 0 and args.rows != w.batch:
+        w = w.with_batch(args.rows)
+        wname = f"{w.name} settings at batch {args.rows}"
     B, V = w.batch, w.vocab
     dev_name, dev_mem, dev_cu = qa.device_info()
     dev_name = device_name(dev_name, dev_cu, dev_mem)
@@ -500,7 +507,7 @@ def main():
         kernel = ("k_part (the streaming kernel; k_decide follows it)" if used == "stream"
                   else "k_row (the row kernel: the whole pick)")
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
-    traffic = committed_traffic(w.name, used)
+    traffic = committed_traffic(w.name, used) if wname == w.name else None
     cpu = None
     parity = None
     if host is not None:
@@ -519,7 +526,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": w.name, "batch": B, "vocab": V, "history": w.hist_len,
+        "config": {"workload": wname, "batch": B, "vocab": V, "history": w.hist_len,
                    "temperature": w.temperature, "top_k": w.top_k, "top_p": w.top_p,
                    "min_p": w.min_p, "repeat_penalty": w.repeat_penalty,
                    "mode": args.mode, "kernels": used, "input_buffers": n_buf,

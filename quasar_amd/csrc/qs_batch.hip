@@ -661,25 +661,29 @@ static bool rows_ok(const qs_batch *b, int row0, int n_rows) {
 }
 
 // The kernels a pick with these arguments takes: the batch's mode, or for AUTO the row
-// kernel when the batch has a row per CU and every sampling row aims at most
-// QS_ROW_AUTO_KSEL candidates (its per-wavefront candidate lists hold a few hundred
-// entries; a row that overflows them takes the full-window path), the streaming kernels
-// when the rows allow them, the split-row kernels otherwise.  `kmax` is the largest candidate target among the
-// sampling rows (1 when every row is greedy).
+// kernel when the batch has a row for at least a quarter of the CUs and every sampling row
+// aims at most QS_ROW_AUTO_KSEL candidates (its per-wavefront candidate lists hold a few
+// hundred entries; a row that overflows them takes the full-window path), the streaming
+// kernels when the rows allow them, the split-row kernels otherwise.  `kmax` is the largest
+// candidate target among the sampling rows (1 when every row is greedy).  The quarter: on
+// MI355X (256 CUs) at 151,936 logits a row, a pick of the row kernel takes about 23 us
+// from 8 to 64 rows (one workgroup per row, each row's latency), the streaming pair 17 us at
+// 8 rows rising to 22 at 48 and 28 at 64.
 static int auto_mode(const qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
                      int n_vocab, int kmax) {
     if (b->mode != QS_MODE_AUTO) return b->mode;
-    if (n_rows >= b->n_cu && kmax <= QS_ROW_AUTO_KSEL &&
+    if (4 * (int64_t)n_rows >= b->n_cu && kmax <= QS_ROW_AUTO_KSEL &&
         qs_row_supported(n_rows, n_vocab, row_stride, d_logits))
         return QS_MODE_ROW;
     return qs_part_supported(n_rows, n_vocab, row_stride, d_logits) ? QS_MODE_STREAM
                                                                     : QS_MODE_SPLIT;
 }
 
-// Wavefronts per row of the row kernel: 16 (one workgroup per CU) up to 1.5 rows per CU,
-// 8 (two per CU, one deciding while the other streams) beyond, when two fit.
+// Wavefronts per row of the row kernel: 16 (one workgroup per CU) up to a row per CU, 8
+// (two per CU, one deciding while the other streams) beyond, when two fit (at 300 rows of
+// 151,936 logits: 48.4 us a pick against 51.5 with a second round of 16-wavefront rows).
 static int row_waves(const qs_batch *b, int n_rows) {
-    return 2 * (int64_t)n_rows <= 3 * (int64_t)b->n_cu || !b->row8 ? 16 : 8;
+    return n_rows <= b->n_cu || !b->row8 ? 16 : 8;
 }
 
 extern "C" {
