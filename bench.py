@@ -42,6 +42,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--
        python bench.py --head [--head-rows B]            (the output layer and the pick:
                                                            B x 2048 hidden states, a
                                                            151,936 x 2048 bf16 matrix)
+       python bench.py --sample-h [--workload full_b1]   (sample.h's pick end to end:
+                                                           host logits in, id out)
        python bench.py --head-exact [--head-exact-rows B] (the output layer at the
                                                            reference's arithmetic, B <= 8
                                                            rows, a Q6_K 151,936 x 2048
@@ -95,6 +97,9 @@ def parse():
     ap.add_argument("--head-exact", action="store_true",
                     help="the output layer at the reference's arithmetic and the pick")
     ap.add_argument("--head-exact-rows", type=int, default=1)
+    ap.add_argument("--sample-h", action="store_true",
+                    help="end-to-end latency of sample.h's quasar_sampler_pick (host logits "
+                         "in, id out) on the workload's settings (default full_b1)")
     ap.add_argument("--kernel-steps", type=int, default=100,
                     help="picks timed kernel by kernel for the roofline")
     return ap.parse_args()
@@ -425,6 +430,59 @@ def head_exact_bench(args):
         bt.close()
 
 
+def sample_h_bench(args):
+    """quasar_sampler_pick as the reference's server calls it once per token: host logits
+    (pageable memory) in, one id out.  Each call copies the row to the device, picks, waits
+    and copies the id back; timed one call at a time on the host clock after a warm-up.
+    The parts are timed on their own as well: the row's copy to the device, the device
+    pick of one row (events on the stream, back to back), and a 4-byte copy back."""
+    import quasar_amd as qa
+    from quasar_amd.workloads import STRESS, WORKLOADS
+    w = dict(WORKLOADS, **STRESS)[args.workload or "full_b1"]
+    V = w.vocab
+    dbuf = qa.DeviceBuffer(4 * V)
+    qa.gen_logits_device(dbuf, V, 0, 1, V, w.dist, w.sigma, w.boost, w.seed)
+    host = dbuf.download(np.float32, V)
+    smp = qa.Sampler()
+    smp.config(*w.params(), seed=int(qa.gen_row_seeds(w.seed, 0, 1)[0]))
+    for _ in range(max(args.warmup, 50)):
+        smp.pick(host)
+    n = max(args.steps, 100)
+    lat = np.empty(n)
+    for i in range(n):
+        t0 = time.perf_counter_ns()
+        smp.pick(host)
+        lat[i] = (time.perf_counter_ns() - t0) / 1e3
+    h2d = np.empty(n)
+    for i in range(n):
+        t0 = time.perf_counter_ns()
+        dbuf.upload(host)
+        h2d[i] = (time.perf_counter_ns() - t0) / 1e3
+    d2h = np.empty(n)
+    for i in range(n):
+        t0 = time.perf_counter_ns()
+        dbuf.download(np.int32, 1)
+        d2h[i] = (time.perf_counter_ns() - t0) / 1e3
+    bt = qa.Batch(1, V, max(1, w.repeat_last_n))
+    bt.config(0, 1, *w.params(), seeds=[1])
+    bt.time_picks([dbuf.ptr], V, 1, V, 200)
+    dev_us = 1e3 * bt.time_picks([dbuf.ptr], V, 1, V, 1000) / 1000
+    bt.close()
+    smp.close()
+    dbuf.free()
+    q = lambda a: {"median": round(float(np.median(a)), 2), "p10": round(float(np.percentile(a, 10)), 2),
+                   "p90": round(float(np.percentile(a, 90)), 2)}
+    print(json.dumps({
+        "metric": "sample.h quasar_sampler_pick latency (host logits in, id out)",
+        "value": float(np.median(lat)), "unit": "us", "n_gpus": 1, "steps": n,
+        "warmup": max(args.warmup, 50), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": w.name, "vocab": V, "row_bytes": 4 * V,
+                   "description": w.description},
+        "call_us": q(lat), "copy_in_us": q(h2d), "id_copy_out_us": q(d2h),
+        "device_pick_us_back_to_back": round(dev_us, 2)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -440,6 +498,8 @@ def main():
         return head_bench(args)
     if args.head_exact:
         return head_exact_bench(args)
+    if args.sample_h:
+        return sample_h_bench(args)
     import quasar_amd as qa
     from quasar_amd.workloads import BENCH_WORKLOAD, STRESS, WORKLOADS
 

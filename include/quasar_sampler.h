@@ -155,6 +155,13 @@ int qs_batch_set_history(qs_batch *b, int row0, int n_rows, const int32_t *ids,
 int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
                   int n_vocab, int32_t *d_out, qs_pick_diag *d_diag);
 
+/* qs_batch_pick for the batch's rows [row0, row0 + n_rows) from logits rows 0 .. n_rows - 1
+ * of d_logits, ids and diagnostics at d_out[0 ..], d_diag[0 ..]: only those rows' states
+ * change.  The retry of rows a pick left at -3 (QS_EAGAIN): pick each again alone, e.g.
+ * row r with row0 = r, n_rows = 1 and its own logits row. */
+int qs_batch_pick_rows(qs_batch *b, int row0, const float *d_logits, int64_t row_stride,
+                       int n_rows, int n_vocab, int32_t *d_out, qs_pick_diag *d_diag);
+
 /* Which kernels qs_batch_pick uses.  AUTO (the default) takes the row kernel for batches
  * of at least one row per CU whose sampling rows have a top-k of at most 256 (or top-k
  * off), the streaming kernels for smaller batches and larger top-k, and the split-row
@@ -180,7 +187,8 @@ int qs_batch_set_state(qs_batch *b, int row, uint64_t rng, const int32_t *hist, 
  * enqueued since the last call surface here: QS_EAGAIN when a row that needed a
  * whole-window scratch slot (a rare fallback; the batch has a few, shared by its rows)
  * could not take one within the wait limit.  Such a row's id is -3 and its generator state
- * and history are unchanged, so picking it again gives the reference's result. */
+ * and history are unchanged, so picking it again (qs_batch_pick_rows, that row alone: the
+ * other rows' states have advanced) gives the reference's result. */
 int qs_batch_synchronize(qs_batch *b);
 
 /* Read one row's generator state and history (oldest first; up to cap ids). */

@@ -264,6 +264,20 @@ class Batch:
         d = (PickDiag * n_rows).from_buffer_copy(raw.tobytes())
         return ids, list(d)
 
+    def pick_rows(self, row0, logits_ptr, row_stride, n_rows, n_vocab, diag=False):
+        """Pick the batch's rows [row0, row0 + n_rows) from logits rows 0 .. n_rows - 1
+        (qs_batch_pick_rows); returns ids (and a list of PickDiag when diag)."""
+        check(self._lib.qs_batch_pick_rows(self._b, row0, logits_ptr, row_stride, n_rows,
+                                           n_vocab, self._out.ptr,
+                                           self._diag.ptr if diag else None),
+              "qs_batch_pick_rows")
+        self.synchronize()
+        ids = self._out.download(np.int32, n_rows)
+        if not diag:
+            return ids
+        raw = self._diag.download(np.uint8, C.sizeof(PickDiag) * n_rows)
+        return ids, list((PickDiag * n_rows).from_buffer_copy(raw.tobytes()))
+
     def synchronize(self):
         check(self._lib.qs_batch_synchronize(self._b), "qs_batch_synchronize")
 

@@ -45,6 +45,7 @@ PROTOS = [
     ("qs_batch_reset", _i, [_vp, _i, _i]),
     ("qs_batch_set_history", _i, [_vp, _i, _i, C.POINTER(C.c_int32), _i]),
     ("qs_batch_pick", _i, [_vp, _vp, _i64, _i, _i, _vp, _vp]),
+    ("qs_batch_pick_rows", _i, [_vp, _i, _vp, _i64, _i, _i, _vp, _vp]),
     ("qs_batch_set_state", _i, [_vp, _i, _u64, C.POINTER(C.c_int32), _i]),
     ("qs_batch_set_mode", _i, [_vp, _i]),
     ("qs_batch_resolve_mode", _i, [_vp, _vp, _i64, _i, _i]),

@@ -572,6 +572,7 @@ struct qs_batch {
     uint32_t *d_hbits = nullptr;           // its history bitmap (zero between picks)
     bool hbits_dirty = false;              // a fused pick failed after marking it: clear
                                            // it before the next one
+    int32_t *h_pin = nullptr;              // pinned: a one-row pick's id and error flag
 };
 
 static void batch_release(qs_batch *b) {
@@ -584,6 +585,7 @@ static void batch_release(qs_batch *b) {
                     b->sc.pcand, b->d_hrec, b->d_hbits};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
+    if (b->h_pin) (void)hipHostFree(b->h_pin);
     if (b->ev0) (void)hipEventDestroy(b->ev0);
     if (b->ev1) (void)hipEventDestroy(b->ev1);
     if (b->stream) (void)hipStreamDestroy(b->stream);
@@ -820,12 +822,13 @@ int qs_batch_get_state(qs_batch *b, int row, uint64_t *rng, int32_t *hist, int c
     return 0;
 }
 
-// The largest top-k among the sampling rows of [0, n_rows) and whether any row samples;
-// QS_EINVAL when a row's ring is larger than the batch holds.
-static int batch_kmax(const qs_batch *b, int n_rows, int *kmax, bool *any_sample) {
+// The largest top-k among the sampling rows of [row0, row0 + n_rows) and whether any row
+// samples; QS_EINVAL when a row's ring is larger than the batch holds.
+static int batch_kmax(const qs_batch *b, int n_rows, int *kmax, bool *any_sample,
+                      int row0 = 0) {
     *kmax = 1;
     *any_sample = false;
-    for (int r = 0; r < n_rows; ++r) {
+    for (int r = row0; r < row0 + n_rows; ++r) {
         const qs_row_param &p = b->h_prm[r];
         if (row_greedy(p)) continue;
         *any_sample = true;
@@ -849,20 +852,25 @@ int qs_batch_resolve_mode(qs_batch *b, const float *d_logits, int64_t row_stride
     return auto_mode(b, d_logits, row_stride, n_rows, n_vocab, kmax);
 }
 
-int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
-                  int n_vocab, int32_t *d_out, qs_pick_diag *d_diag) {
+// The pick of the batch's rows [row0, row0 + n_rows) from logits rows 0 .. n_rows - 1: the
+// kernels see the rows' state from row0 on (parameters, generators, rings, lengths and
+// heads are arrays over the batch's rows), their scratch from its start.
+static int pick_range(qs_batch *b, int row0, const float *d_logits, int64_t row_stride,
+                      int n_rows, int n_vocab, int32_t *d_out, qs_pick_diag *d_diag) {
     if (!b || !d_logits || !d_out) { qs_set_error("qs_batch_pick: null argument"); return QS_EINVAL; }
-    if (n_rows < 1 || n_rows > b->max_rows || n_vocab < 1 || n_vocab > b->max_vocab ||
-        row_stride < n_vocab) {
-        qs_set_error("qs_batch_pick: rows %d (max %d), vocab %d (max %d), stride %lld", n_rows,
-                     b->max_rows, n_vocab, b->max_vocab, (long long)row_stride);
+    if (row0 < 0 || n_rows < 1 || n_rows > b->max_rows - row0 || n_vocab < 1 ||
+        n_vocab > b->max_vocab || row_stride < n_vocab) {
+        qs_set_error("qs_batch_pick: rows [%d, %d) (max %d), vocab %d (max %d), stride %lld",
+                     row0, row0 + n_rows, b->max_rows, n_vocab, b->max_vocab,
+                     (long long)row_stride);
         return QS_EINVAL;
     }
     int kmax = 1;
     bool any_sample = false;
-    if (const int rc = batch_kmax(b, n_rows, &kmax, &any_sample)) return rc;
-    RowState st0{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
-                 b->max_last_n > 0 ? b->max_last_n : 1};
+    if (const int rc = batch_kmax(b, n_rows, &kmax, &any_sample, row0)) return rc;
+    const int rs = b->max_last_n > 0 ? b->max_last_n : 1;
+    RowState st0{b->d_prm + row0, b->d_rng + row0, b->d_ring + (int64_t)row0 * rs,
+                 b->d_hlen + row0, b->d_hhead + row0, rs};
     const int mode = auto_mode(b, d_logits, row_stride, n_rows, n_vocab, kmax);
     if (mode == QS_MODE_ROW) {
         if (!qs_row_supported(n_rows, n_vocab, row_stride, d_logits)) {
@@ -891,8 +899,7 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
         return QS_EDEVICE;
     }
     g.bm_words = g.slice_len / 32;
-    RowState st{b->d_prm, b->d_rng, b->d_ring, b->d_hlen, b->d_hhead,
-                b->max_last_n > 0 ? b->max_last_n : 1};
+    const RowState st = st0;
     const bool vec = ((uintptr_t)d_logits % 16 == 0) && (row_stride % 4 == 0) &&
                      (n_vocab % 4 == 0);
     const dim3 grid(g.slices, n_rows);
@@ -918,6 +925,16 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
     return 0;
 }
 
+int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_rows,
+                  int n_vocab, int32_t *d_out, qs_pick_diag *d_diag) {
+    return pick_range(b, 0, d_logits, row_stride, n_rows, n_vocab, d_out, d_diag);
+}
+
+int qs_batch_pick_rows(qs_batch *b, int row0, const float *d_logits, int64_t row_stride,
+                       int n_rows, int n_vocab, int32_t *d_out, qs_pick_diag *d_diag) {
+    return pick_range(b, row0, d_logits, row_stride, n_rows, n_vocab, d_out, d_diag);
+}
+
 int qs_batch_set_mode(qs_batch *b, int mode) {
     if (!b || mode < QS_MODE_AUTO || mode > QS_MODE_ROW) {
         qs_set_error("qs_batch_set_mode: bad mode %d", mode);
@@ -940,6 +957,32 @@ int qs_batch_synchronize(qs_batch *b) {
                      "pick them again", err);
         return QS_EAGAIN;
     }
+    return 0;
+}
+
+int qs_batch_pick1_host(qs_batch *b, float *d_logits, const float *logits, int n_vocab,
+                        int32_t *d_out, int32_t *id) {
+    if (!b || !d_logits || !logits || !d_out || !id) return QS_EINVAL;
+    if (!b->h_pin)
+        HIP_TRY(hipHostMalloc((void **)&b->h_pin, 2 * sizeof(int32_t), hipHostMallocDefault),
+                "pinned id buffer");
+    HIP_TRY(hipMemcpyAsync(d_logits, logits, sizeof(float) * (size_t)n_vocab,
+                           hipMemcpyHostToDevice, b->stream), "logits to the device");
+    if (const int rc = qs_batch_pick(b, d_logits, n_vocab, 1, n_vocab, d_out, nullptr)) return rc;
+    HIP_TRY(hipMemcpyAsync(b->h_pin, d_out, sizeof(int32_t), hipMemcpyDeviceToHost, b->stream),
+            "id to the host");
+    HIP_TRY(hipMemcpyAsync(b->h_pin + 1, b->sc.err, sizeof(int32_t), hipMemcpyDeviceToHost,
+                           b->stream), "error flag to the host");
+    HIP_TRY(hipStreamSynchronize(b->stream), "one-row pick");
+    if (b->h_pin[1]) {
+        const int32_t zero = 0;
+        (void)hipMemcpy(b->sc.err, &zero, sizeof zero, hipMemcpyHostToDevice);
+        qs_set_error("a whole-window scratch slot was not free in time (flags %d): the row "
+                     "returned -3 and kept its generator state and history; pick it again",
+                     b->h_pin[1]);
+        return QS_EAGAIN;
+    }
+    *id = b->h_pin[0];
     return 0;
 }
 

@@ -58,8 +58,6 @@ constexpr int HT = QS_HEAD_TILE;        // vocabulary columns per tile workgroup
 constexpr int HNW = 8;                  // its wavefronts
 constexpr int HNT = HNW * 64;
 constexpr int HK = 32;                  // embedding elements per stage
-constexpr int HB = QS_HEAD_MAX_ROWS;    // rows at most
-constexpr int HRB = HB / 32;            // 32-row blocks at most
 constexpr int CSP = HT + 4;             // pitch of the staged output block (floats)
 constexpr int TMAX = QS_HEAD_MAX_TILES; // tiles per row at most
 
@@ -74,7 +72,7 @@ struct HeadArgs {
     const uint16_t *w;                  // packed weights (k_head_pack), bf16 bits
     int E, n_rows, V, ntiles;
     float *logits;                      // [n_rows][V] raw logits (written)
-    uint32_t *hb;                       // [HRB][V] history bits, bit r % 32 of row r
+    uint32_t *hb;                       // [QS_HEAD_MAX_ROWS / 32][V] history bits, bit r % 32 of row r
     HeadRec *rec;                       // [n_rows][ntiles]
     int records;                        // 0: logits only
     RowState st;

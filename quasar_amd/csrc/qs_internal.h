@@ -38,6 +38,13 @@ void qs_default_param(qs_row_param *out, uint64_t *rng_out);
  * consumes one); see qs_debug_fail_picks. */
 int qs_debug_take_failure(void);
 
+/* sample.h's pick of one row in one round trip: the host row copied to d_logits on the
+ * batch's stream, the pick of row 0, its id and the batch's error flag copied back into
+ * pinned host memory, one wait.  QS_EAGAIN (the flag cleared) as qs_batch_synchronize. */
+struct qs_batch;
+int qs_batch_pick1_host(struct qs_batch *b, float *d_logits, const float *logits, int n_vocab,
+                        int32_t *d_out, int32_t *id);
+
 /* Thread-local error message used by qs_last_error(). */
 void qs_set_error(const char *fmt, ...);
 

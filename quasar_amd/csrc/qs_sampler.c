@@ -175,17 +175,13 @@ static int host_argmax(const float *logits, int n_vocab) {
 int quasar_sampler_pick(quasar_sampler *s, const float *logits, int n_vocab) {
     if (n_vocab <= 0) return 0;                              /* sample.c:112 */
     int rc = qs_debug_take_failure() ? QS_ENOMEM : qs_ensure(s, n_vocab);
-    if (rc == 0) rc = qs_memcpy_h2d(s->d_logits, logits, sizeof(float) * (size_t)n_vocab);
-    if (rc == 0) rc = qs_batch_pick(s->batch, s->d_logits, n_vocab, 1, n_vocab, s->d_out, NULL);
     int32_t id = -1;
-    if (rc == 0) rc = qs_batch_synchronize(s->batch);
+    /* the row in, the pick, the id and the error flag out, one wait */
+    if (rc == 0) rc = qs_batch_pick1_host(s->batch, s->d_logits, logits, n_vocab, s->d_out, &id);
     /* A whole-window row that found no free scratch slot in time kept its state: pick it
      * again (a one-row batch has its own slot, so this is not expected). */
-    for (int again = 0; rc == QS_EAGAIN && again < 3; ++again) {
-        rc = qs_batch_pick(s->batch, s->d_logits, n_vocab, 1, n_vocab, s->d_out, NULL);
-        if (rc == 0) rc = qs_batch_synchronize(s->batch);
-    }
-    if (rc == 0) rc = qs_memcpy_d2h(&id, s->d_out, sizeof id);
+    for (int again = 0; rc == QS_EAGAIN && again < 3; ++again)
+        rc = qs_batch_pick1_host(s->batch, s->d_logits, logits, n_vocab, s->d_out, &id);
     if (rc == 0 && (id < 0 || id >= n_vocab)) rc = QS_EDEVICE;
     if (rc == 0) {
         host_record(s, id);

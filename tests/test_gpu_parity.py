@@ -428,6 +428,53 @@ def test_bounded_wait_give_up_keeps_state(qa, oracle):
     buf.free()
 
 
+def test_bounded_wait_give_up_multi_row_retry(qa, oracle):
+    """In a batch of 4 rows whose whole-window slot waits all give up (spin limit 0), every
+    whole-window row returns -3 with its state kept; qs_batch_pick_rows then picks each
+    such row alone and it gets the reference's id, while rows a retry does not name keep
+    the state their first pick left."""
+    from quasar_amd.workloads import STRESS
+    w = STRESS["fullwindow_b8"]
+    V, B = w.vocab, 4
+    x = oracle.gen_logits(w.dist, w.sigma, w.boost, w.seed, 0, B, V)
+    buf = qa.DeviceBuffer.from_array(x)
+    b = qa.Batch(B, V, 8)
+    seeds = [0x5EED + r for r in range(B)]
+    for r in range(B):
+        if r == 1:
+            b.config(r, 1, 0.0, 1.0, 0, 0.0, 1.0, 8, seeds=[seeds[r]])   # greedy: no slot
+        else:
+            b.config(r, 1, *w.params(), seeds=[seeds[r]])
+        b.set_history(r, np.array([3 + r, 5, 7], np.int32))
+    before = [b.get_state(r) for r in range(B)]
+    b.set_spin_limit(0)
+    b.pick_async(buf.ptr, V, B, V)
+    with pytest.raises(qa.QsError) as e:
+        b.synchronize()
+    assert e.value.rc == qa.QS_EAGAIN
+    first = b._out.download(np.int32, B)
+    failed = [r for r in range(B) if first[r] == -3]
+    assert 1 not in failed and failed, first
+    for r in failed:
+        after = b.get_state(r)
+        assert after[0] == before[r][0] and list(after[1]) == list(before[r][1]), r
+    kept = {r: b.get_state(r) for r in range(B) if r not in failed}
+    b.set_spin_limit(1 << 20)
+    for r in failed:
+        got = int(b.pick_rows(r, buf.ptr + 4 * V * r, V, 1, V)[0])
+        o = oracle.sampler()
+        o.config(*w.params(), seed=seeds[r])
+        o.set_history([3 + r, 5, 7])
+        assert got == o.pick(x[r]), r
+        rng, h = b.get_state(r)
+        assert rng == o.rng and list(h) == list(o.history()), r
+    for r, st in kept.items():
+        now = b.get_state(r)
+        assert now[0] == st[0] and list(now[1]) == list(st[1]), r
+    b.close()
+    buf.free()
+
+
 def test_sample_h_state_rules(qa, oracle):
     """Config/reset/pick sequences through the five-function API: the ring keeps its
     capacity when repeat_last_n is 0 (sample.c:61-66), reset keeps the generator,
