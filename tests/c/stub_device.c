@@ -35,6 +35,11 @@ int qs_batch_pick(qs_batch *b, const float *d_logits, int64_t row_stride, int n_
     return QS_EDEVICE;
 }
 int qs_batch_synchronize(qs_batch *b) { (void)b; return QS_EDEVICE; }
+int qs_batch_pick1_host(struct qs_batch *b, float *d_logits, const float *logits, int n_vocab,
+                        int32_t *d_out, int32_t *id) {
+    (void)b; (void)d_logits; (void)logits; (void)n_vocab; (void)d_out; (void)id;
+    return QS_EDEVICE;
+}
 int qs_batch_set_state(qs_batch *b, int row, uint64_t rng, const int32_t *hist, int n) {
     (void)b; (void)row; (void)rng; (void)hist; (void)n;
     return QS_EDEVICE;
