@@ -1332,9 +1332,14 @@ __device__ __forceinline__ void decide_row(int row, const qs_row_param &P, const
     int nkept = 0;
     uint32_t rej = t.rej;
     if (!full) {
-        // the row's top K by logit (ties kept); everything dropped raises `rej`
+        // every gathered candidate when they fit the sort, else the row's top K by logit
+        // (ties kept), everything dropped raising `rej`.  Keeping them all matters where
+        // the K-th and the next logit differ but their probabilities round equal: sorted
+        // by (p, id) the dropped one may come first in the reference's order, so its p
+        // bounds the proven prefix below K and the row would take the whole window.
         const int K = row_ksel(P);
-        const uint32_t th = t.total > K ? block_kth<NT>(keys, t.total, K, dl.hist, dl.sh + 4) : 0u;
+        const uint32_t th = t.total > K && t.total > SC
+                                ? block_kth<NT>(keys, t.total, K, dl.hist, dl.sh + 4) : 0u;
         if (tid == 0) { dl.sh[3] = 0; dl.shu[0] = rej; }
         __syncthreads();
         const float inv = (float)(1.0 / t.sum);
