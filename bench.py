@@ -88,6 +88,11 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run plain device copies of --copy-mib MiB (counter calibration)")
     ap.add_argument("--copy-mib", type=int, default=512)
+    ap.add_argument("--copy-kind", choices=["plain", "buffer", "lds", "dword"],
+                    default="plain",
+                    help="the calibration copy's load: plain 16-byte global loads, "
+                         "nontemporal raw buffer loads (the row kernel's), those loads into "
+                         "LDS (the streaming part kernel's), or plain 4-byte loads")
     ap.add_argument("--router", action="store_true",
                     help="only time qs_router_topk (128 experts, 8 used, renormalised)")
     ap.add_argument("--router-tokens", type=int, default=4096)
@@ -116,9 +121,10 @@ def calibrate_copy(args):
     import quasar_amd as qa
     n = args.copy_mib << 20
     src, dst = qa.DeviceBuffer(n), qa.DeviceBuffer(n)
-    qa.copy_device(dst, src, n, 4)
-    print(json.dumps({"calibrate_copy": {"bytes_read": n, "bytes_written": n, "copies": 4}}),
-          flush=True)
+    kind = {"plain": 0, "buffer": 1, "lds": 2, "dword": 3}[args.copy_kind]
+    qa.copy_device(dst, src, n, 4, kind)
+    print(json.dumps({"calibrate_copy": {"bytes_read": n, "bytes_written": n, "copies": 4,
+                                         "load": args.copy_kind}}), flush=True)
 
 
 def committed_traffic(workload, mode):

@@ -278,6 +278,12 @@ int qs_batch_set_spin_limit(qs_batch *b, int attempts);
  * d_src to d_dst, then a device synchronization: a kernel of known memory traffic for
  * calibrating hardware memory counters. */
 int qs_copy_device(void *d_dst, const void *d_src, size_t bytes, int iters);
+/* The same copies with another load instruction: kind 0 plain global loads (as
+ * qs_copy_device), 1 raw buffer loads of 16 bytes, nontemporal (the row kernel's), 2 those
+ * loads written straight into LDS (the streaming part kernel's), 3 plain loads of 4 bytes.
+ * Counters that count a load kind differently are calibrated against the copy of that
+ * kind. */
+int qs_copy_device_kind(void *d_dst, const void *d_src, size_t bytes, int iters, int kind);
 
 /* y[i] = the library's expf(x[i]) on the device, i < n (the softmax numerator routine,
  * exposed so tests can compare it with the host C library's expf). */

@@ -107,10 +107,13 @@ def router_time(logits, n_tokens, n_expert, n_used, norm_topk, idx, wt, iters):
     return ms.value
 
 
-def copy_device(dst, src, nbytes, iters=1):
-    """`iters` plain streaming copies of nbytes from src to dst (DeviceBuffers): a kernel of
-    known memory traffic for calibrating hardware counters."""
-    check(load().qs_copy_device(dst.ptr, src.ptr, nbytes, iters), "qs_copy_device")
+def copy_device(dst, src, nbytes, iters=1, kind=0):
+    """`iters` streaming copies of nbytes from src to dst (DeviceBuffers): a kernel of known
+    memory traffic for calibrating hardware counters; kind 0 plain 16-byte loads, 1
+    nontemporal raw buffer loads, 2 buffer loads into LDS, 3 plain 4-byte loads
+    (qs_copy_device_kind)."""
+    check(load().qs_copy_device_kind(dst.ptr, src.ptr, nbytes, iters, kind),
+          "qs_copy_device_kind")
 
 
 def head_packed_bytes(n_embd, n_vocab):

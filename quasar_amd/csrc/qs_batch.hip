@@ -490,6 +490,45 @@ __global__ void __launch_bounds__(WG) k_copy(const float4 *x, float4 *y, int64_t
         y[i] = x[i];
 }
 
+// The copy in 4-byte elements (plain global loads of one dword).
+__global__ void __launch_bounds__(WG) k_copy1(const float *x, float *y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x; i < n; i += (int64_t)gridDim.x * WG)
+        y[i] = x[i];
+}
+
+// The same copy with the loads of the sampler's streaming kernels, for counter calibration:
+// a raw buffer load of 16 bytes, nontemporal (the row kernel's), or that load written
+// straight into LDS (the streaming part kernel's), each over a buffer resource spanning the
+// workgroup's float4s (loads past it read no memory).
+constexpr int CP_WORD3 = 0x00020000;     // raw buffer, 32-bit data format
+constexpr int CP_NT = 2;                 // nontemporal
+typedef unsigned int cp_u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void cp_lds_void;
+template <bool LDS>
+__global__ void __launch_bounds__(WG) k_copy_buf(const float4 *x, float4 *y, int64_t n4) {
+    __shared__ float4 st[WG];
+    const int tid = threadIdx.x;
+    for (int64_t c = (int64_t)blockIdx.x * WG; c < n4; c += (int64_t)gridDim.x * WG) {
+        const int64_t left = n4 - c;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(x + c), 0, (int)((left < WG ? left : WG) * 16), CP_WORD3);
+        float4 v;
+        if constexpr (LDS) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (cp_lds_void *)(st + (tid & ~63)), 16,
+                                                     tid * 16, 0, 0, CP_NT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            const volatile float *q = (const volatile float *)&st[tid];
+            v = make_float4(q[0], q[1], q[2], q[3]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read before reloaded
+        } else {
+            const cp_u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, tid * 16, 0, CP_NT);
+            v = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                            __uint_as_float(u.w));
+        }
+        if (tid < left) y[c + tid] = v;
+    }
+}
+
 // The kernels' expf, element by element.  Inside [-33, 0] the pipelined kernel's 4-wide
 // window variant (qs_expf4_window, extended table) runs too, and a result different from
 // qs_expf_tab's is reported as NaN, so the comparison with the host C library covers both.
@@ -1366,8 +1405,12 @@ int qs_gen_logits_device(float *d_out, int64_t row_stride, int64_t row0, int n_r
 }
 
 int qs_copy_device(void *d_dst, const void *d_src, size_t bytes, int iters) {
-    if (!d_dst || !d_src || bytes % 16 != 0 || bytes == 0 || iters < 1 ||
-        (uintptr_t)d_dst % 16 != 0 || (uintptr_t)d_src % 16 != 0) {
+    return qs_copy_device_kind(d_dst, d_src, bytes, iters, 0);
+}
+
+int qs_copy_device_kind(void *d_dst, const void *d_src, size_t bytes, int iters, int kind) {
+    if (!d_dst || !d_src || bytes % 16 != 0 || bytes == 0 || iters < 1 || kind < 0 ||
+        kind > 3 || (uintptr_t)d_dst % 16 != 0 || (uintptr_t)d_src % 16 != 0) {
         qs_set_error("qs_copy_device: bad arguments");
         return QS_EINVAL;
     }
@@ -1377,9 +1420,20 @@ int qs_copy_device(void *d_dst, const void *d_src, size_t bytes, int iters) {
     const int64_t n4 = (int64_t)(bytes / 16);
     int64_t blocks = (n4 + WG - 1) / WG;
     if (blocks > (int64_t)ncu * 16) blocks = (int64_t)ncu * 16;
-    for (int i = 0; i < iters; ++i)
-        hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(WG), 0, 0,
-                           (const float4 *)d_src, (float4 *)d_dst, n4);
+    for (int i = 0; i < iters; ++i) {
+        const dim3 g((unsigned)blocks), t(WG);
+        if (kind == 0)
+            hipLaunchKernelGGL(k_copy, g, t, 0, 0, (const float4 *)d_src, (float4 *)d_dst, n4);
+        else if (kind == 1)
+            hipLaunchKernelGGL(k_copy_buf<false>, g, t, 0, 0, (const float4 *)d_src,
+                               (float4 *)d_dst, n4);
+        else if (kind == 2)
+            hipLaunchKernelGGL(k_copy_buf<true>, g, t, 0, 0, (const float4 *)d_src,
+                               (float4 *)d_dst, n4);
+        else
+            hipLaunchKernelGGL(k_copy1, g, t, 0, 0, (const float *)d_src, (float *)d_dst,
+                               4 * n4);
+    }
     HIP_TRY(hipGetLastError(), "k_copy launch");
     HIP_TRY(hipDeviceSynchronize(), "k_copy");
     return 0;
