@@ -274,6 +274,13 @@ int qs_gen_logits_device(float *d_out, int64_t row_stride, int64_t row0, int n_r
  * a million, half a second): a test hook that forces the QS_EAGAIN path with 0. */
 int qs_batch_set_spin_limit(qs_batch *b, int attempts);
 
+/* Rows that leave the certified decision recount their softmax denominator with the
+ * reference's numerators in a fixed order, and again in id order as sample.c adds them
+ * wherever the two orders' rounding could reach a different float normaliser.  With
+ * always = 1 every such row is summed in id order (a test hook: the recount's sum then
+ * equals the reference's bit for bit); 0, the default, only where needed. */
+int qs_batch_set_sum_in_order(qs_batch *b, int always);
+
 /* `iters` plain streaming copies of `bytes` (a multiple of 16, 16-byte aligned) from
  * d_src to d_dst, then a device synchronization: a kernel of known memory traffic for
  * calibrating hardware memory counters. */

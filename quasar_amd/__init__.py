@@ -284,6 +284,12 @@ class Batch:
     def synchronize(self):
         check(self._lib.qs_batch_synchronize(self._b), "qs_batch_synchronize")
 
+    def set_sum_in_order(self, always):
+        """Exact-path rows sum their denominator in id order always (1) or where needed (0)
+        (qs_batch_set_sum_in_order)."""
+        check(self._lib.qs_batch_set_sum_in_order(self._b, int(always)),
+              "qs_batch_set_sum_in_order")
+
     def set_spin_limit(self, attempts):
         """Attempts a row makes at a whole-window scratch slot (qs_batch_set_spin_limit)."""
         check(self._lib.qs_batch_set_spin_limit(self._b, int(attempts)),

@@ -56,6 +56,7 @@ PROTOS = [
     ("qs_row_config_set", None, [_vp, _f, _f, _i, _f, _f, _i]),
     ("qs_pick_noalloc", _i, [_vp, _i64, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     ("qs_batch_set_spin_limit", _i, [_vp, _i]),
+    ("qs_batch_set_sum_in_order", _i, [_vp, _i]),
     ("qs_last_error", C.c_char_p, []),
     ("qs_device_alloc", _vp, [_sz]),
     ("qs_device_free", None, [_vp]),

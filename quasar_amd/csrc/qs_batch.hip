@@ -437,6 +437,19 @@ __global__ void __launch_bounds__(WG) k_finalize(FinArgs a) {
         if (tid == 0) record_greedy(row, P, gbv, gbi, tot.maxl, x[0], st, a.out, a.diag);
         return;
     }
+    // the reference's inv where the slices' fixed-order sum does not settle it
+    {
+        constexpr int BLK = 32768;                         // bitmap block: in fl (not yet used)
+        static_assert(sizeof(FullLds<WG>) >= BLK / 8, "the bitmap in fl");
+        const float msc = tot.maxl * P.inv_t;
+        if (isfinite(msc) && (sc.sum_in_order || !inv_settled(tot.sum, tot.nwin))) {
+            __shared__ double xch;
+            const double s = sum_in_id_order<WG, BLK>(x, g.vocab, st, row, P, msc,
+                                                      (uint32_t *)&fl, dl.tab, &xch);
+            if (tid == 0) tot.sum = s;
+            __syncthreads();
+        }
+    }
     RowTotals t = tot;
     t.total = offs[S];
     if (t.total <= FIN_CAP && isfinite(t.maxl * P.inv_t)) {
@@ -1026,6 +1039,15 @@ int qs_batch_pick1_host(qs_batch *b, float *d_logits, const float *logits, int n
 }
 
 void *qs_batch_stream(qs_batch *b) { return b ? (void *)b->stream : nullptr; }
+
+int qs_batch_set_sum_in_order(qs_batch *b, int always) {
+    if (!b || always < 0 || always > 1) {
+        qs_set_error("qs_batch_set_sum_in_order: bad arguments");
+        return QS_EINVAL;
+    }
+    b->sc.sum_in_order = always;
+    return 0;
+}
 
 int qs_batch_set_spin_limit(qs_batch *b, int attempts) {
     if (!b || attempts < 0) {

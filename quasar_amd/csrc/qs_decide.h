@@ -134,7 +134,12 @@ __device__ __forceinline__ void row_visit(const PartArgs &a, int row, const qs_r
 
 // The row's exact softmax denominator and window size (sample.c:136-149), recomputed from
 // the logits with the host-libm-equal expf: for rows the certified decision does not cover.
-// All threads; the sums reduce in a fixed order.
+// All threads; the sums reduce in a fixed order.  That order's sum and the reference's
+// (ids ascending) are sums of the same n nonnegative binary64 numbers, each within
+// (n - 1) 2^-53 of their exact total, so the two differ by at most 2 n 2^-53 of it; where
+// (float)(1 / x) is the same float at both ends of that reach it is the reference's inv
+// (1 / x and both roundings are monotone), and where it is not (or sc.sum_in_order asks
+// for it) the sum is taken again in id order.
 __device__ __forceinline__ void exact_totals(const PartArgs &a, int row, const qs_row_param &P, float msc,
                              DecLds &dl, double &sum, int &nwin) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -158,6 +163,9 @@ __device__ __forceinline__ void exact_totals(const PartArgs &a, int row, const q
     sum = s;
     nwin = c;
     __syncthreads();
+    if (a.sc.sum_in_order || !inv_settled(s, c))   // (uniform)
+        sum = sum_in_id_order<ND, XBM>(a.logits + (int64_t)row * a.stride, a.vocab, a.st, row,
+                                       P, msc, dl.bm, dl.dl.tab, &dl.exs[0]);
 }
 
 // The block's (largest value, first index) of (v, i) pairs; i < 0: none.  All threads.

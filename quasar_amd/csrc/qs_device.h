@@ -478,6 +478,8 @@ struct Scratch {
     int nslots;
     int ccap;             // candidates per slice list
     int spin_limit;       // full-window slot lock: attempts before giving up
+    int sum_in_order;     // 1: the exact path always sums the denominator in id order (a
+                          // test hook); 0: only when its fixed-order sum leaves inv open
 };
 
 struct Geometry {
@@ -1615,6 +1617,79 @@ __device__ __forceinline__ void decide_row_fast(int row, const qs_row_param &P, 
                            fixed_slot);
     else if (status == 2)
         full_row<NT>(x, V, row, P, t.maxl, t.sum, st, sc, out, diag, dl.tab, fl, fixed_slot);
+}
+
+// Whether a fixed-order binary64 sum s of n nonnegative numbers gives the reference's
+// inv = (float)(1 / sum) (sample.c:149), whose sum adds the same numbers in id order: both
+// sums lie within (n - 1) 2^-53 of the numbers' exact total, so within 2 n 2^-53 of each
+// other, and (float)(1 / x) is monotone in x, so one float at both ends of that reach is
+// the reference's.
+__device__ __forceinline__ bool inv_settled(double s, int n) {
+    const double reach = 2.0 * (double)n * 0x1p-53 * s * (1.0 + 0x1p-20);
+    return (float)(1.0 / (s - reach)) == (float)(1.0 / (s + reach));
+}
+
+// The row's softmax denominator exactly as sample.c:147-149 adds it: the window's
+// numerators in id order, one binary64 addition after another (a numerator outside the
+// window is 0 here and adds nothing).  All NT threads of the workgroup take part in the
+// history bitmaps (blocks of BLK logits in `bm`, BLK / 32 words); wavefront 0 computes 64
+// numerators at a time and adds them in order, lane by lane.  About 1 ms for 151,936
+// logits: taken only where the fixed-order sum does not settle inv (inv_settled).  `xch`:
+// one double of LDS for the result.
+template <int NT, int BLK>
+__device__ __forceinline__ double sum_in_id_order(const float *x, int V, const RowState &st,
+                                                  int row, const qs_row_param &P, float msc,
+                                                  uint32_t *bm, const uint64_t *tab,
+                                                  double *xch) {
+    static_assert(BLK % 64 == 0, "whole batches of 64 ids a block");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const float rp = P.repeat_penalty, inv_t = P.inv_t, thr = msc - 30.0f;
+    const int cap = P.ring_cap;                   // (clamped: row_param)
+    int len, head;
+    ring_pos(st, row, cap, len, head);
+    const bool pen = rp > 1.0f && len > 0 && cap > 0;
+    const int32_t *ring = st.ring + (int64_t)row * st.ring_stride;
+    double acc = 0.0;
+    for (int lo = 0; lo < V; lo += BLK) {
+        const int hi = min(lo + BLK, V);
+        if (pen) {                                    // sample.c:118-120: each id once
+            for (int j = tid; j < BLK / 32; j += NT) bm[j] = 0u;
+            __syncthreads();
+            for (int j = tid; j < len; j += NT) {
+                const int id = ring[qs_ring_slot(cap, head, j)];
+                if (id >= lo && id < hi) atomicOr(&bm[(id - lo) >> 5], 1u << ((id - lo) & 31));
+            }
+            __syncthreads();
+        }
+        if (tid < 64) {
+            for (int b0 = lo; b0 < hi; b0 += 64) {
+                const int id = b0 + lane;
+                double e = 0.0;
+                if (id < hi) {
+                    float w = x[id];
+                    const int q = id - lo;
+                    if (pen && ((bm[q >> 5] >> (q & 31)) & 1u)) w = penalise(w, rp);
+                    const float sc = w * inv_t;
+                    if (sc >= thr) e = (double)qs_expf_core(sc - msc, tab);
+                }
+                const uint64_t eb = (uint64_t)__double_as_longlong(e);
+                const int lo32 = (int)(uint32_t)eb, hi32 = (int)(uint32_t)(eb >> 32);
+                const int n = min(64, hi - b0);
+                for (int j = 0; j < n; ++j) {         // (uniform) ids b0, b0 + 1, ... in turn
+                    const uint64_t v =
+                        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi32, j) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane(lo32, j);
+                    acc += __longlong_as_double((long long)v);
+                }
+            }
+        }
+        if (pen) __syncthreads();                     // the block's bitmap is read
+    }
+    if (tid == 0) *xch = acc;
+    __syncthreads();
+    const double r = *xch;
+    __syncthreads();
+    return r;
 }
 
 // sample.c:130-134 from per-slice (value, first index) bests: nothing beats a NaN at index

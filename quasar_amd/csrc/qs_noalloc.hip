@@ -121,6 +121,7 @@ int qs_pick_noalloc(const float *d_logits, int64_t row_stride, int n_rows, int n
     sc.nslots = QS_NOALLOC_SLOTS;
     sc.ccap = 0;
     sc.spin_limit = SPIN_LIMIT;
+    sc.sum_in_order = 0;
     static_assert(sizeof(qs_row_config) == sizeof(qs_row_param), "row config layout");
     // the kernels clamp each row's ring capacity to ring_stride (0: no ring, whatever the
     // row configs say) and its history length and head to that capacity (qs_ring.h), so

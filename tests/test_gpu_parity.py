@@ -475,6 +475,45 @@ def test_bounded_wait_give_up_multi_row_retry(qa, oracle):
     buf.free()
 
 
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("name", ["fullwindow_b8", "nucleus_b8", "minp_only_b8"])
+def test_exact_path_sum_in_id_order(qa, oracle, mode, name):
+    """Rows that leave the certified decision, with the recount's in-id-order sum forced
+    (qs_batch_set_sum_in_order): each such row's denominator equals the restatement's
+    (sample.c:147-149, ids ascending) bit for bit, and so do its id and state, under every
+    mode (AUTO, split, streaming, row)."""
+    from quasar_amd.workloads import STRESS
+    w = STRESS[name]
+    B, V = w.batch, w.vocab
+    x = oracle.gen_logits(w.dist, w.sigma, w.boost, w.seed, 0, B, V)
+    buf = qa.DeviceBuffer.from_array(x)
+    b = qa.Batch(B, V, max(1, w.repeat_last_n))
+    b.set_mode(mode)
+    seeds = qa.gen_row_seeds(w.seed, 0, B)
+    b.config(0, B, *w.params(), seeds=seeds)
+    hist = qa.gen_history(w.seed, 0, B, w.hist_len, V, w.hist_pool) if w.hist_len else None
+    if hist is not None:
+        b.set_history(0, hist)
+    b.set_sum_in_order(1)
+    ids, diag = b.pick(buf.ptr, V, B, V, diag=True)
+    exact = 0
+    for r in range(B):
+        s = oracle.sampler()
+        s.config(*w.params(), seed=int(seeds[r]))
+        if hist is not None:
+            s.set_history(hist[r])
+        want, od = s.pick_diag(x[r])
+        assert int(ids[r]) == want, (r, int(ids[r]), want)
+        if diag[r].path in (qa.PATH_FAST, qa.PATH_FULL):
+            exact += 1
+            assert diag[r].sum == od["sum"], (r, diag[r].sum, od["sum"])
+            assert np.float32(diag[r].inv) == np.float32(od["inv"]), r
+    log(f"{name} mode {mode}: {exact} of {B} rows on the exact path, sums equal")
+    assert exact > 0
+    b.close()
+    buf.free()
+
+
 def test_sample_h_state_rules(qa, oracle):
     """Config/reset/pick sequences through the five-function API: the ring keeps its
     capacity when repeat_last_n is 0 (sample.c:61-66), reset keeps the generator,
