@@ -26,6 +26,10 @@ Also reported on the same JSON line:
                 measured for the same workload and kernels (profiles/traffic.json, written
                 from rocprofv3 FETCH_SIZE and WRITE_SIZE runs scaled by the same counters
                 on a copy of known size; null when no such measurement is committed)
+  read_ceiling  when the pick is the row kernel at one row per CU: the same rows read by
+                a kernel with the row kernel's launch shape, chunks and loads that only
+                adds them up (qs_time_row_reads), its time and rate, and the pick's time
+                over it (the part of the pick the sampling itself costs)
   cpu_baseline  the reference's own sample.c (oracle/_ref, when built) or the CPU
                 restatement over a bounded sample of the same rows, on the host's cores
                 (at most 16 threads: a one-GPU share of the box) and on one core, with the
@@ -573,6 +577,16 @@ def main():
         kernel = ("k_part (the streaming kernel; k_decide follows it)" if used == "stream"
                   else "k_row (the row kernel: the whole pick)")
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
+    # the row pick's loads alone at its launch shape: the read ceiling of the same bytes
+    read = None
+    if used == "row" and B <= dev_cu:
+        qa.time_row_reads(ptrs, V, B, V, 50)
+        read_ms = qa.time_row_reads(ptrs, V, B, V, args.steps) / args.steps
+        read_gbs = 4 * B * V / (read_ms * 1e-3) / 1e9
+        read = {"kernel": "k_row_read (the row kernel's launch shape, chunks and loads, "
+                          "adding the rows up and nothing else)",
+                "ms": read_ms, "achieved": read_gbs, "unit": "GB/s",
+                "frac": read_gbs / HBM_PEAK_GBS, "pick_over_read": ms_per_step / read_ms}
     traffic = committed_traffic(w.name, used) if wname == w.name else None
     cpu = None
     parity = None
@@ -604,6 +618,7 @@ def main():
                      "traffic_source": traffic["source"] if traffic else None,
                      "kernel": kernel, "kernel_ms": kernel_ms, "pick_frac": pick_frac,
                      "bytes_per_step": alg_bytes},
+        "read_ceiling": read,
         "cpu_baseline": cpu,
         "parity": parity,
         "paths": {str(k): v for k, v in sorted(paths.items())},

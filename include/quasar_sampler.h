@@ -292,6 +292,19 @@ int qs_copy_device(void *d_dst, const void *d_src, size_t bytes, int iters);
  * kind. */
 int qs_copy_device_kind(void *d_dst, const void *d_src, size_t bytes, int iters, int kind);
 
+/* The row pick's loads alone: `iters` back-to-back launches on the null stream, launch i
+ * reading d_logits[i % n_buffers] (n_rows rows of n_vocab floats, row_stride apart, as
+ * qs_batch_pick takes them) with the row kernel's launch shape at one row per CU (one
+ * workgroup of 16 wavefronts per row), its chunks and its load instruction (raw 16-byte
+ * nontemporal buffer loads, two chunks in flight a wavefront), adding up each row's floats
+ * and nothing else.  *ms: the elapsed milliseconds of all launches (HIP events).  The
+ * same bytes read at the same shape without the sampling: the ceiling a row pick's time is
+ * compared with.  d_sink: n_rows floats, written only for a sum no finite row reaches.
+ * Needs 16-byte aligned rows, n_vocab and row_stride multiples of 4 (QS_EINVAL otherwise).
+ * No counterpart in the reference: a measurement aid. */
+int qs_time_row_reads(const float *const *d_logits, int n_buffers, int64_t row_stride,
+                      int n_rows, int n_vocab, float *d_sink, int iters, float *ms);
+
 /* y[i] = the library's expf(x[i]) on the device, i < n (the softmax numerator routine,
  * exposed so tests can compare it with the host C library's expf). */
 int qs_expf_device(const float *d_x, float *d_y, int64_t n);

@@ -107,6 +107,23 @@ def router_time(logits, n_tokens, n_expert, n_used, norm_topk, idx, wt, iters):
     return ms.value
 
 
+def time_row_reads(logits_ptrs, row_stride, n_rows, n_vocab, iters):
+    """The row pick's loads alone (qs_time_row_reads): `iters` launches of a kernel with the
+    row kernel's launch shape, chunks and loads that only adds up the rows, launch i reading
+    logits_ptrs[i % len].  Returns the elapsed milliseconds of all launches."""
+    if isinstance(logits_ptrs, int):
+        logits_ptrs = [logits_ptrs]
+    arr = (C.c_void_p * len(logits_ptrs))(*logits_ptrs)
+    sink = DeviceBuffer(4 * n_rows)
+    ms = C.c_float(0)
+    try:
+        check(load().qs_time_row_reads(arr, len(logits_ptrs), row_stride, n_rows, n_vocab,
+                                       sink.ptr, iters, C.byref(ms)), "qs_time_row_reads")
+    finally:
+        sink.free()
+    return ms.value
+
+
 def copy_device(dst, src, nbytes, iters=1, kind=0):
     """`iters` streaming copies of nbytes from src to dst (DeviceBuffers): a kernel of known
     memory traffic for calibrating hardware counters; kind 0 plain 16-byte loads, 1

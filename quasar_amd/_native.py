@@ -76,6 +76,7 @@ PROTOS = [
     ("qs_expf_device", _i, [_vp, _vp, _i64]),
     ("qs_copy_device", _i, [_vp, _vp, _sz, _i]),
     ("qs_copy_device_kind", _i, [_vp, _vp, _sz, _i, _i]),
+    ("qs_time_row_reads", _i, [C.POINTER(_vp), _i, _i64, _i, _i, _vp, _i, C.POINTER(C.c_float)]),
     ("qs_router_topk", _i, [_vp, _i64, _i, _i, _i, _i, _vp, _vp, _vp]),
     ("qs_router_time", _i, [_vp, _i64, _i, _i, _i, _i, _vp, _vp, _i, C.POINTER(C.c_float)]),
     ("qs_head_packed_bytes", _sz, [_i, _i]),

@@ -720,7 +720,84 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
     exact_row(a, row, P, t, dl, hist, status);
 }
 
+// The row pick's loads alone, for the read ceiling its streaming is measured against: the
+// row kernel's launch shape at one row per CU (one workgroup of 16 wavefronts per row), its
+// chunks, load instruction and order (two chunks in flight a wavefront, the next taken from
+// the row's LDS counter, the partial last chunk by the last wavefront), each lane's floats
+// added up and nothing else.  sink[row] is written only for a sum no row of finite logits
+// reaches, so the loads stay and the kernel writes nothing.
+__global__ void __launch_bounds__(1024) k_row_read(const float *logits, int64_t stride,
+                                                    int vocab, float *sink) {
+    constexpr int NW = 16;
+    __shared__ int next;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n4 = vocab >> 2, nch = (n4 + RCH - 1) / RCH, nr = n4 / RCH;
+    const float *rowp = logits + (int64_t)row * stride;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)rowp, 0, n4 * 16, BUF_WORD3);
+    float4 A[RU], B[RU], T[RU];
+    int jA = wv, jB = NW + wv;
+    if (nr < nch && wv == NW - 1) load_chunk(T, rs, nr, lane);
+    load_chunk(A, rs, jA, lane);
+    load_chunk(B, rs, jB, lane);
+    if (tid == 0) next = 2 * NW;
+    lds_barrier();
+    float s = 0.0f;
+    auto add = [&](float4 (&X)[RU]) {
+#pragma unroll
+        for (int u = 0; u < RU; ++u) s += (X[u].x + X[u].y) + (X[u].z + X[u].w);
+    };
+    auto take = [&]() {
+        int j = 0;
+        if (lane == 0) j = atomicAdd(&next, 1);
+        return __builtin_amdgcn_readfirstlane(j);
+    };
+    if (nr < nch && wv == NW - 1) add(T);             // (past the row the loads read 0)
+    for (;;) {
+        if (jA >= nr) break;
+        add(A);
+        jA = take();
+        load_chunk(A, rs, jA, lane);
+        if (jB >= nr) break;
+        add(B);
+        jB = take();
+        load_chunk(B, rs, jB, lane);
+    }
+    if (s == -0x1.234p120f) sink[row] = s;
+}
+
 }  // namespace
+
+int qs_time_row_reads(const float *const *d_logits, int n_buffers, int64_t row_stride,
+                      int n_rows, int n_vocab, float *d_sink, int iters, float *ms) {
+    if (!d_logits || n_buffers < 1 || !d_sink || iters < 1 || !ms || n_rows < 1 ||
+        row_stride < n_vocab) {
+        qs_set_error("qs_time_row_reads: bad arguments");
+        return QS_EINVAL;
+    }
+    for (int i = 0; i < n_buffers; ++i)
+        if (!d_logits[i] || !qs_row_supported(n_rows, n_vocab, row_stride, d_logits[i])) {
+            qs_set_error("qs_time_row_reads: buffer %d is not a row kernel input", i);
+            return QS_EINVAL;
+        }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = 0;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) rc = QS_EDEVICE;
+    if (!rc && hipEventRecord(e0, 0) != hipSuccess) rc = QS_EDEVICE;
+    for (int i = 0; i < iters && !rc; ++i) {
+        hipLaunchKernelGGL(k_row_read, dim3((unsigned)n_rows), dim3(1024), 0, 0,
+                           d_logits[i % n_buffers], row_stride, n_vocab, d_sink);
+        if (hipGetLastError() != hipSuccess) rc = QS_EDEVICE;
+    }
+    if (!rc && (hipEventRecord(e1, 0) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                hipEventElapsedTime(ms, e0, e1) != hipSuccess))
+        rc = QS_EDEVICE;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (rc) qs_set_error("qs_time_row_reads: device error");
+    return rc;
+}
 
 int qs_row_resident(int waves) {
     int nb = 0;
