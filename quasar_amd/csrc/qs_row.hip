@@ -295,10 +295,21 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
                     const int f = f0 + u * 64 + lane;
                     const uint32_t nib = (wd[u] >> ((f & 7) * 4)) & 0xFu;
                     float w[4] = {X[u].x, X[u].y, X[u].z, X[u].w};
+                    if (__ballot((nib & (nib - 1u)) != 0u)) {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const float v = penalise_r(w[k], rp, rinv);
-                        w[k] = (nib >> k) & 1u ? v : w[k];
+                        for (int k = 0; k < 4; ++k) {
+                            const float v = penalise_r(w[k], rp, rinv);
+                            w[k] = (nib >> k) & 1u ? v : w[k];
+                        }
+                    } else {
+                        // at most one history id per lane in this group: penalise that one
+                        const bool h1 = nib == 2u, h2 = nib == 4u, h3 = nib == 8u;
+                        const float x = h1 ? w[1] : h2 ? w[2] : h3 ? w[3] : w[0];
+                        const float v = penalise_r(x, rp, rinv);
+                        w[0] = nib == 1u ? v : w[0];
+                        w[1] = h1 ? v : w[1];
+                        w[2] = h2 ? v : w[2];
+                        w[3] = h3 ? v : w[3];
                     }
                     X[u] = make_float4(w[0], w[1], w[2], w[3]);
                 }
