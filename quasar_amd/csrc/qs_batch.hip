@@ -542,6 +542,17 @@ __global__ void __launch_bounds__(WG) k_copy_buf(const float4 *x, float4 *y, int
     }
 }
 
+// A one-row pick's result for the host: its id and the batch's error flag stored by one
+// thread into pinned host memory (h: the device's address of it), in place of two
+// device-to-host copies.
+__global__ void __launch_bounds__(64) k_result1(const int32_t *out, const int32_t *err,
+                                                int32_t *h) {
+    if (threadIdx.x == 0) {
+        h[0] = out[0];
+        h[1] = err[0];
+    }
+}
+
 // The kernels' expf, element by element.  Inside [-33, 0] the pipelined kernel's 4-wide
 // window variant (qs_expf4_window, extended table) runs too, and a result different from
 // qs_expf_tab's is reported as NaN, so the comparison with the host C library covers both.
@@ -625,6 +636,7 @@ struct qs_batch {
     bool hbits_dirty = false;              // a fused pick failed after marking it: clear
                                            // it before the next one
     int32_t *h_pin = nullptr;              // pinned: a one-row pick's id and error flag
+    int32_t *d_pin = nullptr;              // the device's address of h_pin
 };
 
 static void batch_release(qs_batch *b) {
@@ -1015,16 +1027,22 @@ int qs_batch_synchronize(qs_batch *b) {
 int qs_batch_pick1_host(qs_batch *b, float *d_logits, const float *logits, int n_vocab,
                         int32_t *d_out, int32_t *id) {
     if (!b || !d_logits || !logits || !d_out || !id) return QS_EINVAL;
-    if (!b->h_pin)
+    if (!b->h_pin) {
         HIP_TRY(hipHostMalloc((void **)&b->h_pin, 2 * sizeof(int32_t), hipHostMallocDefault),
                 "pinned id buffer");
+        if (hipHostGetDevicePointer((void **)&b->d_pin, b->h_pin, 0) != hipSuccess) {
+            (void)hipHostFree(b->h_pin);
+            b->h_pin = nullptr;
+            b->d_pin = nullptr;
+            qs_set_error("pinned id buffer: no device address");
+            return QS_EDEVICE;
+        }
+    }
     HIP_TRY(hipMemcpyAsync(d_logits, logits, sizeof(float) * (size_t)n_vocab,
                            hipMemcpyHostToDevice, b->stream), "logits to the device");
     if (const int rc = qs_batch_pick(b, d_logits, n_vocab, 1, n_vocab, d_out, nullptr)) return rc;
-    HIP_TRY(hipMemcpyAsync(b->h_pin, d_out, sizeof(int32_t), hipMemcpyDeviceToHost, b->stream),
-            "id to the host");
-    HIP_TRY(hipMemcpyAsync(b->h_pin + 1, b->sc.err, sizeof(int32_t), hipMemcpyDeviceToHost,
-                           b->stream), "error flag to the host");
+    hipLaunchKernelGGL(k_result1, dim3(1), dim3(64), 0, b->stream, d_out, b->sc.err, b->d_pin);
+    HIP_TRY(hipGetLastError(), "k_result1 launch");
     HIP_TRY(hipStreamSynchronize(b->stream), "one-row pick");
     if (b->h_pin[1]) {
         const int32_t zero = 0;
