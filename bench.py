@@ -18,11 +18,14 @@ input (--buffers, default: more than 512 MiB in total) that each pick reads from
 Also reported on the same JSON line:
   roofline      for the pick's dominant kernel (the row kernel k_row, the whole pick, or
                 the streaming kernel k_part): algorithmic bytes per launch (4V logits + 4H
-                history + 4 id + 16 RNG per row) over its average duration, timed with HIP
-                events on the batch's stream around each of --kernel-steps further picks
-                (an event before the pick, one after k_row or between the streaming pick's
-                two kernels), against 8 TB/s HBM; `pick_frac` is the same bytes over the
-                whole pick; `traffic` is the HBM bytes per pick that hardware counters
+                history + 4 id + 16 RNG per row) over its average duration, against 8 TB/s
+                HBM.  The row kernel is one launch a step: its average duration is the timed
+                region's (HIP events on the batch's stream over the back-to-back launches);
+                `kernel_ms_isolated` is each of --kernel-steps further launches timed alone
+                (an event before it, one after it), which adds a start from an idle queue.
+                The streaming kernel k_part is timed alone that way, with an event between
+                the pick's two kernels.  `pick_frac` is the same bytes over the whole pick;
+                `traffic` is the HBM bytes per pick that hardware counters
                 measured for the same workload and kernels (profiles/traffic.json, written
                 from rocprofv3 FETCH_SIZE and WRITE_SIZE runs scaled by the same counters
                 on a copy of known size; null when no such measurement is committed)
@@ -572,10 +575,18 @@ def main():
     alg_bytes = B * w.algorithmic_bytes_per_row()
     pick_frac = alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
     kernel_ms, kernel = ms_per_step, f"one pick ({KERNELS[used]})"
-    if used in ("stream", "row") and args.kernel_steps > 0:
+    kernel_ms_isolated = None
+    if used == "row":
+        # the row kernel is the whole pick, one launch a step: the timed region's events over
+        # the back-to-back launches give its average duration (a kernel trace of the same run
+        # shows each launch starting as the previous one ends)
+        kernel = "k_row (the row kernel: the whole pick, launches back to back)"
+        if args.kernel_steps > 0:
+            kernel_ms_isolated = (batch.time_stream_kernel(ptrs, V, B, V, args.kernel_steps)
+                                  / args.kernel_steps)
+    elif used == "stream" and args.kernel_steps > 0:
         kernel_ms = batch.time_stream_kernel(ptrs, V, B, V, args.kernel_steps) / args.kernel_steps
-        kernel = ("k_part (the streaming kernel; k_decide follows it)" if used == "stream"
-                  else "k_row (the row kernel: the whole pick)")
+        kernel = "k_part (the streaming kernel; k_decide follows it)"
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     # the row pick's loads alone at its launch shape: the read ceiling of the same bytes
     read = None
@@ -616,7 +627,8 @@ def main():
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
-                     "kernel": kernel, "kernel_ms": kernel_ms, "pick_frac": pick_frac,
+                     "kernel": kernel, "kernel_ms": kernel_ms,
+                     "kernel_ms_isolated": kernel_ms_isolated, "pick_frac": pick_frac,
                      "bytes_per_step": alg_bytes},
         "read_ceiling": read,
         "cpu_baseline": cpu,
