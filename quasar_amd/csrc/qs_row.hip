@@ -403,10 +403,10 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
             // the row's threshold: a ratchet over the published maxima (the 4 NW 16-lane
             // maxima, each a distinct logit, or with rat_lane every lane's running maximum),
             // raised only when at least kp of them lie strictly above the new value (so at
-            // least kp logits of the row do); seeded once kp are published, one key below
-            // the least 16-lane maximum or below the kp-th largest lane maximum.  A
-            // wavefront's first chunk also takes the m_first-th largest lane maximum of that
-            // chunk (below).
+            // least kp logits of the row do).  It starts at the largest first-chunk bound a
+            // wavefront has entered (below), or, before any has, at a seed once kp are
+            // published: one key below the least 16-lane maximum or below the kp-th largest
+            // lane maximum.
             uint32_t pv = 0u;
             if (rat_lane) {
                 rl.pub[wv * 64 + lane] = run;
@@ -453,13 +453,20 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
                     lds_st(&rl.rstep, st > 1u ? st >> 1 : 1u);
                 }
             }
-            // before the ratchet is seeded a wavefront keeps the m0-th largest lane maximum
-            // of its first chunk, m0 = 6 or ceil(K / 8) (of one chunk only: the running
-            // maxima of several chunks hold more of the row's largest logits, and a bound
-            // that high leaves fewer than K logits above the row's bound; a chunk's 6th
-            // largest lies above a row's 200th largest logit in a few rows in a hundred)
-            if (first) th0 = wave_mth(run, wmx, m_first);
-            th = first ? max(rt, th0) : (rt ? rt : th0);
+            // a wavefront's first chunk takes at least th0, the m_first-th largest lane
+            // maximum of that chunk, m_first = 6 or ceil(K / 8) (of one chunk only: the
+            // running maxima of several chunks hold more of the row's largest logits, and a
+            // bound that high leaves fewer than K logits above the row's bound; a chunk's 6th
+            // largest lies above a row's 200th largest logit in a few rows in a hundred).
+            // Its rejections put th0 - 1 into the row's rejected bound, so every later chunk
+            // of the row may take at least th0 too: a logit below it would only be gathered
+            // to be dropped.  th0 enters the shared threshold (the ratchet then climbs from
+            // it, each raise still proved by kp published maxima, and needs no seed).
+            if (first) {
+                th0 = wave_mth(run, wmx, m_first);
+                if (lane == 0 && th0 > rt) atomicMax(&rl.rth, th0);
+            }
+            th = max(rt, th0);
             first = 0;
         } else {
             // this wavefront's statistic, capped by the others' published ones
