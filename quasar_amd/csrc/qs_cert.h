@@ -46,6 +46,10 @@ namespace qs {
 
 constexpr float CERT_L = 0x1.715476p+0f;          // float(log2 e) = 1.44269502162933349609375
 constexpr double CERT_LN2 = 0x1.62e42fefa39efp-1;
+// 1 / L in binary64 (folded by the compiler, rounded to nearest): A below is multiplied by
+// it instead of divided by L, one rounding of 2^-53 in place of the division's, inside the
+// factor 1 + 2^-22 that covers A's arithmetic.
+constexpr double CERT_INV_L = 1.0 / (double)CERT_L;
 // KAPPA_A above (1.32559e-7), rounded up.
 constexpr double CERT_KAPPA_A = 1.3256e-7;
 // Host expf (glibc 2.35 x86-64): largest relative error over every float in [-64, 0],
@@ -148,7 +152,7 @@ __device__ __forceinline__ CertPart cert_part(float maxw, double S, float T, flo
     const double arho = -rho;
     // sum of e^_i a_i: a_i <= (|t_i| (1 + 2^-23) + |rho|) / L; T carries at most about
     // 30 roundings of 2^-24 (20 fma steps per thread, then the reductions)
-    const double A = ((double)T * (1.0 + 0x1p-18) + arho * sup) / (double)CERT_L * (1.0 + 0x1p-22);
+    const double A = ((double)T * (1.0 + 0x1p-18) + arho * sup) * CERT_INV_L * (1.0 + 0x1p-22);
     const double kj = 0x1p-24 * (CERT_LN2 * arho + D) + CERT_ZETA + CERT_ETA + 0x1p-100;
     const double E = s * (1.0 + 0x1p-10) * (CERT_KAPPA_A * A + kj * sup);
     r.lo = s * slo - E;
@@ -171,23 +175,35 @@ __device__ __forceinline__ float cert_cbase(float M) {
 // of fl(sc L - c'), at most 2^-24 |sc L - c'| <= 2^-24 |sc L - c|, so the per-element bound
 // of cert_part holds with this rho.  T = sum of e^ * (-t) is an approximation whose
 // roundings (a float chain per chunk, then binary64 rescaling and sums) stay far inside
-// the factor 1 + 2^-12 allowed for them.
-__device__ __forceinline__ CertPart cert_part_c(float maxw, float c, double S, double T,
-                                                float inv_t, float msc, float thr) {
+// the factor 1 + 2^-12 allowed for them.  cert_part_cs takes the part's scale
+// s = exp(-D - rho ln 2) (D = msc - M) from cert_scale_c, which needs neither sum, so a
+// caller may compute it while the sums are still being reduced; cert_part_c does both.
+__device__ __forceinline__ double cert_scale_c(float maxw, float c, float inv_t, float msc) {
+    const float M = maxw * inv_t;
+    const double rho = (double)CERT_L * (double)M - (double)c;     // exact in binary64
+    const double D = (double)msc - (double)M;                      // exact, >= 0
+    return exp(-D - rho * CERT_LN2);
+}
+
+__device__ __forceinline__ CertPart cert_part_cs(float maxw, float c, double S, double T,
+                                                 float inv_t, float msc, float thr, double s) {
     CertPart r{0.0, 0.0};
     const float M = maxw * inv_t;
     if (!(M >= thr) || !(S > 0.0)) return r;
     const double rho = (double)CERT_L * (double)M - (double)c;     // exact in binary64
     const double D = (double)msc - (double)M;                      // exact, >= 0
-    const double s = exp(-D - rho * CERT_LN2);
     const double sup = S * (1.0 + 0x1.12p-23), slo = S * (1.0 - 0x1.12p-23);
     const double arho = -rho;
-    const double A = (T * (1.0 + 0x1p-12) + arho * sup) / (double)CERT_L * (1.0 + 0x1p-22);
+    const double A = (T * (1.0 + 0x1p-12) + arho * sup) * CERT_INV_L * (1.0 + 0x1p-22);
     const double kj = 0x1p-24 * (CERT_LN2 * arho + D) + CERT_ZETA + CERT_ETA + 0x1p-100;
     const double E = s * (1.0 + 0x1p-10) * (CERT_KAPPA_A * A + kj * sup);
     r.lo = s * slo - E;
     r.hi = s * sup + E;
     return r;
+}
+__device__ __forceinline__ CertPart cert_part_c(float maxw, float c, double S, double T,
+                                                float inv_t, float msc, float thr) {
+    return cert_part_cs(maxw, c, S, T, inv_t, msc, thr, cert_scale_c(maxw, c, inv_t, msc));
 }
 
 // The whole-row interval from the per-part sums of lo/hi: the window's outside elements

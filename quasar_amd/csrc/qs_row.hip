@@ -568,25 +568,15 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
     } else if (wv != NW - 1) {
         // the candidates above the row's bound (below it every list is incomplete and
         // counts as rejected) appended to the gathered arrays with their exact numerators
-        // (any order: every decision selects and sorts): the lists' entries flattened over
-        // the threads of every wavefront but the last, which takes the row's totals
-        const int cl = lane < NW ? min(rl.seg[lane].cnt, WCAP) : 0;
-        const int incl = wave_scan(cl);             // lanes < NW: lists 0..lane's entries
-        const int n_all = __builtin_amdgcn_readlane(incl, NW - 1);
-        uint32_t ends[NW];
-#pragma unroll
-        for (int v = 0; v < NW; ++v) ends[v] = (uint32_t)__builtin_amdgcn_readlane(incl, v);
-        for (int f0 = 0; f0 < n_all; f0 += (NW - 1) * 64) {
-            const int f = f0 + tid;                 // tid < (NW - 1) * 64 here
-            int w = 0;
-#pragma unroll
-            for (int v = 0; v < NW - 1; ++v) w += (uint32_t)f >= ends[v];
-            const int i = f - (w > 0 ? (int)ends[w > 0 ? w - 1 : 0] : 0);
-            const bool valid = f < n_all;
+        // (any order: every decision selects and sorts): each wavefront but the last takes
+        // its own list, and the last one's list (that wavefront takes the row's totals) is
+        // dealt out to them in slices of 64
+        auto gather = [&](int w, int i, int n) {    // entry i of list w, which holds n
+            const bool valid = i < n;
             const uint32_t kv = valid ? rl.ckey[w][i] : 0u;
             const bool hit = valid && kv > rej_row;
             const uint64_t mk = __ballot(hit);
-            if (mk == 0ull) continue;
+            if (mk == 0ull) return;
             const int idv = hit ? rl.cid[w][i] : 0;
             const float e = hit && cert_ok ? cert_e(kv, inv_t, msc, thr, rl.tab) : 0.0f;
             const uint64_t mw = __ballot(e > 0.0f);
@@ -602,18 +592,26 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
                 rl.dl.ids[pos] = idv;
                 if (pos < WAVE_CAND) rl.gk[pos] = e > 0.0f ? eid_key(e, idv) : 0ull;
             }
-        }
+        };
+        const int own = __builtin_amdgcn_readfirstlane(min(rl.seg[wv].cnt, WCAP));
+        const int last = __builtin_amdgcn_readfirstlane(min(rl.seg[NW - 1].cnt, WCAP));
+        for (int i0 = 0; i0 < own; i0 += 64) gather(wv, i0 + lane, own);
+        for (int i0 = wv * 64; i0 < last; i0 += (NW - 1) * 64) gather(NW - 1, i0 + lane, last);
     }
     QS_TL_HOOK(9);
+    if (wv == NW - 2 && lane == 0)                  // the rejected logits' numerator bound
+        rl.e_rej = cert_ok && rej_row > KEY_NEG_INF ? cert_e(rej_row, inv_t, msc, thr, rl.tab)
+                                                    : 0.0f;
     if (wv == NW - 1) {
         // the row's totals from the segments' records: one certified part (every segment's
-        // sums moved exactly to the row's base, the largest), the denominator interval, the
-        // window size when every segment lies wholly in or out of the window, and the
-        // numerator bound of the rejected logits
+        // sums moved exactly to the row's base, the largest), the denominator interval and
+        // the window size when every segment lies wholly in or out of the window
         const bool have = lane < NW;
         const SegRec r = rl.seg[have ? lane : 0];
         const float maxw = have ? key2f(r.maxk) : -INFINITY;
         const float cr = wave_max_f(have ? r.c : C_INIT);
+        // the part's scale needs neither sum: every lane computes it while the sums reduce
+        const double s_row = cert_scale_c(maxl, cr, inv_t, msc);
         const float d = have ? cr - r.c : 0.0f;
         const int sh = -(int)fminf(d, 4096.0f);
         const double Sx = have ? ldexp(r.sum, sh) : 0.0;
@@ -629,7 +627,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
             t.msc = msc;
             double S_lo = 1.0, S_hi = 1.0;
             if (!greedy) {
-                const CertPart cp = cert_part_c(maxl, cr, S_row, T_row, inv_t, msc, thr);
+                const CertPart cp = cert_part_cs(maxl, cr, S_row, T_row, inv_t, msc, thr, s_row);
                 cert_interval(cp.lo, cp.hi, msc, thr, V, S_lo, S_hi);
             }
             t.S_lo = S_lo;
@@ -642,9 +640,6 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
             t.total = 0;
             rl.ct = t;
         }
-        if (lane == 32)                             // the rejected logits' numerator bound
-            rl.e_rej = cert_ok && rej_row > KEY_NEG_INF ? cert_e(rej_row, inv_t, msc, thr, rl.tab)
-                                                        : 0.0f;
     }
     QS_TL_HOOK(10);
     lds_barrier();
