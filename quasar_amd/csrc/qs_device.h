@@ -313,6 +313,24 @@ __device__ __forceinline__ void wave_scan3(double &a, double &b, double &c) {
 #undef QS_SCAN3
 }
 
+// Reductions over lanes 0-15 (quad permutes, the half-row and the row mirror): every one
+// of lanes 0-15 ends with the combination of all sixteen, read from lane 0.
+template <typename T, typename F>
+__device__ __forceinline__ T lane16_reduce(T v, F &&op) {
+    v = op(v, dpp_move<0xB1, 0xF>(v));
+    v = op(v, dpp_move<0x4E, 0xF>(v));
+    v = op(v, dpp_move<0x141, 0xF>(v));
+    v = op(v, dpp_move<0x140, 0xF>(v));
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, 0);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 0);
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
+
 // Reductions over lanes 0-7 (quad permutes, then the half-row mirror): every one of lanes
 // 0-7 ends with the combination of all eight, read from lane 0.
 template <typename T, typename F>

@@ -163,6 +163,7 @@ __device__ __forceinline__ int row_m(const qs_row_param &P, int nw) {
 // workgroups per CU.
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) k_row(PartArgs a) {
+    static_assert(NW <= 16, "the segment records are reduced over lanes 0-15");
     __shared__ RowLds<NW> rl;
     constexpr int WCAP = RowLds<NW>::WCAP;
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -549,10 +550,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
     TL_ROW(4);
     QS_TL_HOOK(8);
     // every wavefront: the row's max, window threshold, rejected bound and list overflow
-    const uint32_t rmx = wave_max_u(lane < NW ? rl.seg[lane].maxk : 0u);
+    auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+    const uint32_t rmx = lane16_reduce(lane < NW ? rl.seg[lane].maxk : 0u, umax);
     const float maxl = key2f(rmx > KEY_NEG_INF ? rmx : KEY_NEG_INF);
     const float msc = maxl * inv_t, thr = msc - 30.0f;
-    const uint32_t rej_row = wave_max_u(lane < NW ? rl.seg[lane].rej : 0u);
+    const uint32_t rej_row = lane16_reduce(lane < NW ? rl.seg[lane].rej : 0u, umax);
     const bool cflag = __ballot(lane < NW && rl.seg[lane].cnt > WCAP) != 0ull;
     const bool cert_ok = !greedy && isfinite(msc) && fabsf(msc) < CERT_MSC_MAX && !cflag;
     const int nl = min(rl.seg[wv].cnt, WCAP);
@@ -609,18 +611,20 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
         const bool have = lane < NW;
         const SegRec r = rl.seg[have ? lane : 0];
         const float maxw = have ? key2f(r.maxk) : -INFINITY;
-        const float cr = wave_max_f(have ? r.c : C_INIT);
+        const float cr = lane16_reduce(have ? r.c : C_INIT, [](float x, float y) { return fmaxf(x, y); });
         // the part's scale needs neither sum: every lane computes it while the sums reduce
         const double s_row = cert_scale_c(maxl, cr, inv_t, msc);
         const float d = have ? cr - r.c : 0.0f;
         const int sh = -(int)fminf(d, 4096.0f);
         const double Sx = have ? ldexp(r.sum, sh) : 0.0;
         const double Tx = have ? ldexp(r.term + (double)d * r.sum, sh) : 0.0;
-        const double S_row = wave_sum_d(Sx), T_row = wave_sum_d(Tx);
+        auto dsum = [](double x, double y) { return x + y; };
+        const double S_row = lane16_reduce(Sx, dsum), T_row = lane16_reduce(Tx, dsum);
         const bool out_j = !(maxw * inv_t >= thr);
         const bool in_j = have && r.mink != 0xFFFFFFFFu && key2f(r.mink) * inv_t >= thr;
         const bool known = __ballot(have && !out_j && !in_j) == 0ull;
-        const int nin = wave_sum_i(have && !out_j && in_j ? r.len - r.nan : 0);
+        const int nin = lane16_reduce(have && !out_j && in_j ? r.len - r.nan : 0,
+                                      [](int x, int y) { return x + y; });
         if (lane == 0) {
             CertTotals t;
             t.maxl = maxl;
@@ -672,7 +676,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
             for (; q < total; q += G) cnt += rl.gk[q] > kc;
         }
         QS_TL_HOOK(6);
-        for (int o = 1; o < G; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+        // the G lanes of a candidate (consecutive, G a power of two up to 16) add up
+        if (G > 1) cnt += dpp_move<0xB1, 0xF>(cnt);     // lane ^ 1
+        if (G > 2) cnt += dpp_move<0x4E, 0xF>(cnt);     // lane ^ 2: quads
+        if (G > 4) cnt += dpp_move<0x141, 0xF>(cnt);    // half-row mirror: eights
+        if (G > 8) cnt += dpp_move<0x140, 0xF>(cnt);    // row mirror: sixteens
         if (g == 0 && kc != 0ull) {
             if (cnt < 64) rl.dl.srt[cnt] = kc;
             else if (cnt == 64) rl.e64 = key_p(kc);
