@@ -8,8 +8,9 @@
 // wavefronts finish together.  At launch each wavefront requests its first chunk together
 // with the history ring's first slots; the second goes out once the history bitmap is
 // built.  No wavefront waits for another until the row is done:
-//   1. the repeat penalty from the row's history bitmap in LDS and each chunk's list of
-//      history positions (sample.c:118-128); each lane's max and min (NaN-propagating);
+//   1. the repeat penalty from the row's history bitmap in LDS and each chunk's mask of the
+//      float4 groups holding a history id (sample.c:118-128); each lane's max and min
+//      (NaN-propagating);
 //   2. sampling rows: per logit sc = w * inv_t, t = fl(sc * L - c), e = 2^t (v_exp_f32),
 //      summed in float quads then binary64, and e * t, against the wavefront's integer
 //      exponent base c >= its running max * L; when a chunk raises the base the sums are
