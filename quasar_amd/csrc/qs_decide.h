@@ -79,6 +79,7 @@ struct DecLds {
     float pterm[QS_PART_MAX_PARTS];
     uint32_t pmin[QS_PART_MAX_PARTS];
     int pnan[QS_PART_MAX_PARTS];
+    int gcount;                          // decide_par: candidates gathered
 };
 static_assert(sizeof(FullLds<ND>) <= sizeof(uint32_t) * 2 * FCAP, "full-window LDS aliases keys/ids");
 

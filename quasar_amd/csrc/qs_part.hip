@@ -735,6 +735,130 @@ __device__ __forceinline__ int decide_wave0(const PartArgs &a, int row, const qs
                          hist);
 }
 
+// The decision of a sampling row of at most 16 parts by the whole workgroup: wavefront 0
+// totals the parts' records into the denominator interval while wavefronts 1-3 gather the
+// candidates above the row's bound into LDS, each from a third of every list's entries;
+// then wavefront 0 takes the certified decision (cert_row_wave).  All threads call it;
+// returns (in wavefront 0) DS_DONE, DS_BLOCK (the block decision or the exact path must
+// run), or a CF_* reason, with dl.ct and the gathered candidates in place.
+__device__ __forceinline__ int decide_par(const PartArgs &a, int row, const qs_row_param &P,
+                                          DecLds &dl, const RowHist &hist) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    static_assert(ND == 256 && WCAP == 32, "three gathering wavefronts, 16 uint4 a list");
+    const Scratch &sc = a.sc;
+    const int NP = a.parts, NL = NP * NWV;
+    const int64_t l0 = (int64_t)row * NP * NWV;
+    // uint4s (two entries) of a list taken by wavefronts 1, 2, 3: [0, 5), [5, 10), [10, 16)
+    const int u0 = wv == 0 ? 0 : 5 * (wv - 1), u1 = wv == 3 ? WCAP / 2 : 5 * wv;
+    WaveRec r[2];
+    uint4 q[2][6];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int L = h * 64 + lane;
+        if (L < NL) {
+            r[h] = sc.wrec[l0 + L];
+            if (wv > 0) {
+                const uint4 *src = (const uint4 *)(sc.pcand + (l0 + L) * WCAP);
+#pragma unroll
+                for (int i = 0; i < 6; ++i)
+                    if (u0 + i < u1) q[h][i] = src[u0 + i];
+            }
+        } else {
+            r[h].sum = 0.0;
+            r[h].term = 0.0f;
+            r[h].mink = 0xFFFFFFFFu;
+            r[h].nan = 0;
+            r[h].maxk = 0u;
+            r[h].rej = 0u;
+            r[h].cnt = 0;
+        }
+    }
+    if (tid == 0) dl.gcount = 0;
+    lds_barrier();                                // the counter (the loads stay in flight)
+    QS_DEC_MARK(1);
+    const bool ovf = __ballot(r[0].cnt > WCAP || r[1].cnt > WCAP) != 0ull;
+    if (wv == 0) {
+        // each part's totals over its NWV consecutive lanes (a fixed order), then the row's
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            double ps = r[h].sum;
+            float pt = r[h].term;
+            uint32_t pmn = r[h].mink;
+            int pn = r[h].nan;
+            group8([&](auto &&mv) {
+                ps += mv(ps);
+                pt += mv(pt);
+                pmn = min(pmn, mv(pmn));
+                pn += mv(pn);
+            });
+            const int L = h * 64 + lane;
+            if ((lane & (NWV - 1)) == 0 && L < NL) {
+                const int j = L / NWV;
+                dl.pmaxk[j] = r[h].maxk;
+                dl.prej[j] = r[h].rej;
+                dl.psum[j] = ps;
+                dl.pterm[j] = pt;
+                dl.pmin[j] = pmn;
+                dl.pnan[j] = pn;
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+        const bool have = lane < NP;
+        CertTotals t = row_totals(a, P, false, have, have ? dl.pmaxk[lane] : 0u,
+                                  have ? dl.psum[lane] : 0.0, have ? dl.pterm[lane] : 0.0f,
+                                  have ? dl.pmin[lane] : 0xFFFFFFFFu, have ? dl.pnan[lane] : 0,
+                                  have ? dl.prej[lane] : 0u);
+        t.cflag = ovf;
+        if (lane == 0) dl.ct = t;
+    } else {
+        // this wavefront's entries above the row's bound (the largest part bound: below it
+        // the lists are incomplete and everything there counts as rejected), counted, placed
+        // by one atomic and stored
+        const uint32_t rj = wave_max_u(max(r[0].rej, r[1].rej));
+        const int c[2] = {min(r[0].cnt, WCAP), min(r[1].cnt, WCAP)};
+        auto each = [&](auto &&f) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 6; ++i) {
+                    if (u0 + i >= u1) continue;
+                    const int j = 2 * (u0 + i);
+                    if (j < c[h] && q[h][i].x > rj) f(q[h][i].x, (int)q[h][i].y);
+                    if (j + 1 < c[h] && q[h][i].z > rj) f(q[h][i].z, (int)q[h][i].w);
+                }
+        };
+        int k = 0;
+        each([&](uint32_t, int) { ++k; });
+        const int incl = wave_scan(k);
+        const int tot = __builtin_amdgcn_readlane(incl, 63);
+        int base = 0;
+        if (lane == 0 && tot > 0) base = atomicAdd(&dl.gcount, tot);
+        base = __builtin_amdgcn_readfirstlane(base);
+        int at = base + incl - k;
+        each([&](uint32_t kv, int id) {
+            if (at < FCAP) {
+                dl.keys[at] = kv;
+                dl.ids[at] = id;
+            }
+            ++at;
+        });
+    }
+    lds_barrier();
+    QS_DEC_MARK(2);
+    const int total = dl.gcount;
+    if (wv != 0) return 0;                        // (the caller reads wavefront 0's status)
+    CertTotals t = dl.ct;
+    t.total = total;
+    if (lane == 0) dl.ct.total = total;
+    QS_DEC_MARK(3);
+    if (!isfinite(t.msc)) return CF_INPUT;
+    if (!(fabsf(t.msc) < CERT_MSC_MAX) || total > FCAP) return CF_MSC;
+    if (row_ksel(P) > 64 || total > WAVE_CAND) return DS_BLOCK;
+    return cert_row_wave(row, P, t, dl.keys, dl.ids, dl.srt, dl.dl.tab, a.st, a.out, a.diag,
+                         hist);
+}
+
 __global__ void __launch_bounds__(ND) k_decide(PartArgs a) {
     __shared__ DecLds dl;
     QS_DEC_MARK(0);
@@ -753,9 +877,14 @@ __global__ void __launch_bounds__(ND) k_decide(PartArgs a) {
     if (NL <= 128) {
         // rows of up to 16 parts: wavefront 0 gathers and decides; the workgroup joins only
         // for the block decision, a greedy row's scan or the exact path
-        if (wv == 0) {
-            const int s0 = decide_wave0(a, row, P, dl, hist);
-            if (lane == 0) dl.dl.sh[7] = s0;
+        if (greedy) {
+            if (wv == 0) {
+                const int s0 = decide_wave0(a, row, P, dl, hist);
+                if (lane == 0) dl.dl.sh[7] = s0;
+            }
+        } else {
+            const int s0 = decide_par(a, row, P, dl, hist);
+            if (tid == 0) dl.dl.sh[7] = s0;
         }
         __syncthreads();
         const int s0 = dl.dl.sh[7];
