@@ -48,11 +48,14 @@ using namespace qs::dec;
 
 namespace {
 
-constexpr int RU = 5;                    // float4 per lane per chunk
+// float4 per lane per chunk: 5 with 16 wavefronts a row (one row a CU), 6 with 8 (two rows a
+// CU, where larger chunks, so fewer per-chunk steps, measured faster; both fit 128 VGPRs)
+template <int NW>
+constexpr int row_ru() { return NW == 8 ? 6 : 5; }
+constexpr int RU = row_ru<16>();         // the 16-wavefront chunk (the read ceiling's too)
 constexpr int RCH = 64 * RU;             // float4 per chunk
 constexpr int ROW_VMAX = QS_ROW_MAX_VOCAB;   // longest row (its history bitmap is in LDS)
 constexpr int RBM = ROW_VMAX / 32 + 4;   // bitmap words
-constexpr int NCH_MAX = (ROW_VMAX / 4 + RCH - 1) / RCH;   // chunks of the longest row
 constexpr uint32_t RATCHET_STEP = 1u << 17;   // the threshold ratchet's first step (keys)
 constexpr int LIST_CAP = 2048;           // candidates all of a row's lists hold (16
                                          // wavefronts; 8 wavefronts: twice that, two
@@ -102,7 +105,8 @@ struct RowLds {
         uint32_t bm[RBM];                // streaming: the row's history ids (bit per logit)
         DecLds dl;                       // decision (the bitmap is dead by then)
     };
-    uint32_t hitu[NCH_MAX];              // chunk j: bit u set when its float4 group u holds a
+    static constexpr int NCH = (ROW_VMAX / 4 + 64 * row_ru<NW>() - 1) / (64 * row_ru<NW>());
+    uint32_t hitu[NCH];                  // chunk j: bit u set when its float4 group u holds a
                                          // history id
     int next;                            // the row's next chunk to take
     uint32_t theta[NW];                  // published running thresholds (keys)
@@ -136,11 +140,13 @@ __device__ __forceinline__ float4 bload(__amdgpu_buffer_rsrc_t rs, int off) {
     return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
                        __uint_as_float(v.w));
 }
-// Chunk j of a segment into registers (lane l, float4 u: segment float4 j*RCH + u*64 + l).
-__device__ __forceinline__ void load_chunk(float4 (&X)[RU], __amdgpu_buffer_rsrc_t rs, int j,
+// Chunk j of a segment into registers (lane l, float4 u of U: segment float4
+// j*64*U + u*64 + l).
+template <int U>
+__device__ __forceinline__ void load_chunk(float4 (&X)[U], __amdgpu_buffer_rsrc_t rs, int j,
                                            int lane) {
 #pragma unroll
-    for (int u = 0; u < RU; ++u) X[u] = bload(rs, (j * RCH + u * 64 + lane) * 16);
+    for (int u = 0; u < U; ++u) X[u] = bload(rs, (j * 64 * U + u * 64 + lane) * 16);
 }
 
 template <typename T>
@@ -165,6 +171,7 @@ __device__ __forceinline__ int row_m(const qs_row_param &P, int nw) {
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) k_row(PartArgs a) {
     static_assert(NW <= 16, "the segment records are reduced over lanes 0-15");
+    constexpr int RU = row_ru<NW>(), RCH = 64 * RU;   // this kernel's chunk
     __shared__ RowLds<NW> rl;
     constexpr int WCAP = RowLds<NW>::WCAP;
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
