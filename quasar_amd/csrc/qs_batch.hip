@@ -646,7 +646,8 @@ static void batch_release(qs_batch *b) {
                     b->sc.bestv, b->sc.besti, b->sc.sth, b->sc.ckey, b->sc.cid, b->sc.ccnt,
                     b->sc.crej, b->sc.cflag, b->sc.psum, b->sc.pcnt, b->sc.locks,
                     b->sc.full_keys, b->sc.full_bm, b->sc.err, b->sc.wrec,
-                    b->sc.pcand, b->d_hrec, b->d_hbits};
+                    b->sc.pcand, b->sc.gbest, b->sc.gmaxk, b->sc.gcnt, b->d_hrec,
+                    b->d_hbits};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     if (b->h_pin) (void)hipHostFree(b->h_pin);
@@ -705,8 +706,14 @@ static int batch_alloc(qs_batch *b) {
     if (!rc) rc = dev_alloc(&b->sc.full_keys, (size_t)b->sc.nslots * 2 * V, "full_keys");
     if (!rc) rc = dev_alloc(&b->sc.full_bm, (size_t)b->sc.nslots * (V / 32 + 1), "full_bm");
     if (!rc) rc = dev_alloc(&b->sc.err, 1, "err");
+    if (!rc) rc = dev_alloc(&b->sc.gbest, R, "greedy bests");
+    if (!rc) rc = dev_alloc(&b->sc.gmaxk, R, "greedy maxima");
+    if (!rc) rc = dev_alloc(&b->sc.gcnt, R, "greedy part counts");
     if (!rc && hipMemset(b->sc.locks, 0, sizeof(int32_t) * b->sc.nslots) != hipSuccess) rc = QS_EDEVICE;
     if (!rc && hipMemset(b->sc.err, 0, sizeof(int32_t)) != hipSuccess) rc = QS_EDEVICE;
+    if (!rc && hipMemset(b->sc.gbest, 0, sizeof(uint64_t) * R) != hipSuccess) rc = QS_EDEVICE;
+    if (!rc && hipMemset(b->sc.gmaxk, 0, sizeof(uint32_t) * R) != hipSuccess) rc = QS_EDEVICE;
+    if (!rc && hipMemset(b->sc.gcnt, 0, sizeof(uint32_t) * R) != hipSuccess) rc = QS_EDEVICE;
     return rc;
 }
 
@@ -950,7 +957,7 @@ static int pick_range(qs_batch *b, int row0, const float *d_logits, int64_t row_
             return QS_EINVAL;
         }
         return qs_part_launch(d_logits, row_stride, n_rows, n_vocab, st0, b->sc, d_out, d_diag,
-                              b->part_resident, b->stream, b->mid);
+                              b->part_resident, b->stream, b->mid, !any_sample);
     }
     Geometry g;
     g.logits = d_logits;

@@ -493,6 +493,12 @@ struct Scratch {
     int32_t *err;         // [1] sticky error flag (a full-window slot wait gave up)
     WaveRec *wrec;        // [rows*parts*8] streaming kernel: per-wavefront results
     uint2 *pcand;         // [rows*parts*256] streaming kernel: (key, id) candidates
+    // [rows] streaming kernel, greedy rows decided by their last part (null: by k_decide):
+    // the largest (penalised key, ~id) over the parts done, their largest max key, and the
+    // parts done; zero between picks (the last part resets them)
+    uint64_t *gbest;
+    uint32_t *gmaxk;
+    uint32_t *gcnt;
     int nslots;
     int ccap;             // candidates per slice list
     int spin_limit;       // full-window slot lock: attempts before giving up

@@ -26,11 +26,13 @@ int qs_part_resident(void);
 // Enqueue the streaming pick on `stream`: the streaming kernel over a grid of about
 // `resident` workgroups, then the decision kernel (ordinary launches: no workgroup waits
 // for another).
-// `mid`, when given, is recorded on the stream between the two kernels (timing).
+// `mid`, when given, is recorded on the stream between the two kernels (timing).  When
+// every row is greedy (`all_greedy`) and sc.gbest is set, each row is decided by its last
+// part in the streaming kernel and the decision kernel is not launched.
 int qs_part_launch(const float *logits, int64_t row_stride, int n_rows, int n_vocab,
                    const qs::RowState &st, const qs::Scratch &sc, int32_t *out,
                    qs_pick_diag *diag, int resident, hipStream_t stream,
-                   hipEvent_t mid = nullptr);
+                   hipEvent_t mid = nullptr, bool all_greedy = false);
 
 // ---- the row kernel (qs_row.hip) ----
 

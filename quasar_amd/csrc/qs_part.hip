@@ -90,6 +90,12 @@ struct StreamArgs {
     const int32_t *ring, *hlen, *hhead;
     WaveRec *rec;
     uint2 *cand;
+    // greedy rows decided by their last part (gbest null: by k_decide), and what that
+    // decision writes: the rows' rings, lengths and heads, ids and diagnostics
+    uint64_t *gbest;
+    uint32_t *gmaxk, *gcnt;
+    int32_t *ring_w, *hlen_w, *hhead_w, *out;
+    qs_pick_diag *diag;
 };
 
 constexpr int PART_BM = bitmap_words(PART_MAX);
@@ -103,6 +109,7 @@ struct PartLds {
     uint32_t theta;                  // a short part's threshold key
     WaveRec rec[NWV];                // each wavefront's record of the last part, and
     uint2 cand[NWV][WCAP];           // its candidates, stored out during the next part
+    uint64_t gbw[2][NWV];            // greedy rows: per-wave (key, ~id) best, by parity
 };
 
 struct Loc {                          // a part of a row
@@ -308,6 +315,28 @@ __device__ __forceinline__ Pass1 pass1(float4 (&buf)[UP], const Loc &l, const ui
     return r;
 }
 
+// A greedy row's part is done (one thread): its best (key, ~id) and max key join the
+// row's by device-wide atomic maxima, each performed before the part is counted; the part
+// that counts last reads the row's best and records it (sample.c:130-134) and resets the
+// three for the next pick.  No part waits for another.
+__device__ __forceinline__ void greedy_part_done(const StreamArgs &a, int row, const qs_row_param &P,
+                                              uint32_t pmk, const uint64_t *gbw) {
+    uint64_t pb = 0ull;
+    for (int j = 0; j < NWV; ++j) pb = gbw[j] > pb ? gbw[j] : pb;
+    const uint64_t ob = atomicMax((unsigned long long *)&a.gbest[row], (unsigned long long)pb);
+    const uint32_t om = atomicMax(&a.gmaxk[row], pmk);
+    asm volatile("s_waitcnt vmcnt(0)" ::"v"(ob), "v"(om) : "memory");   // both performed
+    if (atomicAdd(&a.gcnt[row], 1u) != (uint32_t)a.parts - 1u) return;
+    const uint64_t best = atomicExch((unsigned long long *)&a.gbest[row], 0ull);
+    const uint32_t mk = atomicExch(&a.gmaxk[row], 0u);
+    atomicExch(&a.gcnt[row], 0u);
+    const int bi = best != 0ull ? (int)~(uint32_t)best : -1;
+    const float bv = best != 0ull ? key2f((uint32_t)(best >> 32)) : -INFINITY;
+    const RowState st{a.prm, nullptr, a.ring_w, a.hlen_w, a.hhead_w, a.ring_stride};
+    record_greedy(row, P, bv, bi, key2f(mk > KEY_NEG_INF ? mk : KEY_NEG_INF),
+                  a.logits[(int64_t)row * a.stride], st, a.out, a.diag);
+}
+
 // The candidate rule.  Wavefront w of a part offers th_w, the m-th largest of its 64 lane
 // maxima (so at least m of its logits reach th_w); the part keeps every logit at or above
 // min_w th_w, at least NWV*m logits and in practice about twice that.  m follows the part's
@@ -324,7 +353,7 @@ __device__ __forceinline__ int part_m(const qs_row_param &P, int parts) {
 // barrier, then `mid` (the caller's bitmap upkeep), the part's max and threshold, the sums
 // (sampling rows), the candidates and the wavefront's record.  Nothing here waits for
 // another wavefront after the barrier.
-template <typename Mid>
+template <bool GF, typename Mid>
 __device__ __forceinline__ void part_step(float4 (&buf)[UP], const StreamArgs &a, const Loc &l,
                                           const qs_row_param &P, const uint32_t *bm,
                                           const uint32_t *hitw, int par, PartLds &pl, Mid &&mid,
@@ -358,6 +387,26 @@ __device__ __forceinline__ void part_step(float4 (&buf)[UP], const StreamArgs &a
     }
     const uint32_t wmn = wave_min_u(r.mn == INFINITY ? 0xFFFFFFFFu : f2key(r.mn));
     const int wnan = __ballot(r.nan != 0) ? wave_sum_i(r.nan) : 0;
+    const bool gfuse = GF && greedy;               // (GF: every row of the pick is greedy)
+    if (gfuse) {
+        // sample.c:130-132 over this wavefront's share: the largest penalised logit, the
+        // first id among equals (NaNs never; -0 equals +0, so both take +0's key), as the
+        // largest (key, ~id)
+        uint64_t g = 0ull;
+#pragma unroll
+        for (int u = 0; u < UP; ++u) {
+            const int c = l.c_lo + u * NT + tid;
+            const float w[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t wk = f2key(w[k] == 0.0f ? 0.0f : w[k]);
+                const uint64_t gk = ((uint64_t)wk << 32) | (uint32_t)~(uint32_t)(4 * c + k);
+                if (c < l.c_hi && w[k] == w[k] && gk > g) g = gk;
+            }
+        }
+        g = wave_reduce(g, [](uint64_t x, uint64_t y) { return x > y ? x : y; });
+        if (lane == 0) pl.gbw[par][wv] = g;
+    }
     TL_PART(tl, 2);
     lds_barrier();
     TL_PART(tl, 3);
@@ -386,6 +435,7 @@ __device__ __forceinline__ void part_step(float4 (&buf)[UP], const StreamArgs &a
         th = pl.theta;
     }
     if (th <= KEY_NEG_INF) th = KEY_NEG_INF + 1u;
+    if (gfuse && tid == 0) greedy_part_done(a, l.row, P, pmk, pl.gbw[par]);
     const float M = key2f(pmk) * inv_t;
     // the sums: approximate numerators and e * t, float4 by float4
     double S = 0.0;
@@ -458,8 +508,10 @@ __device__ __forceinline__ void flush_part(const StreamArgs &a, PartLds &pl, int
 // barrier, so one barrier per part orders every bitmap access.
 //
 // The pointers come as separate restrict arguments: with them the row parameters, history
-// lengths and heads (uniform addresses, never written here) are scalar loads, which the
-// wavefront waits for without waiting for the logit loads in flight.
+// lengths and heads (uniform addresses) are scalar loads, which the wavefront waits for
+// without waiting for the logit loads in flight.  They are written only by a greedy row's
+// last part (GF), through other pointers, once every part of the row has read them.
+template <bool GF>
 __global__ void __launch_bounds__(NT, 6)
 k_part(StreamArgs sa, const float *__restrict__ logits, const qs_row_param *__restrict__ prm,
        const int32_t *__restrict__ ring, const int32_t *__restrict__ hlen,
@@ -525,7 +577,7 @@ k_part(StreamArgs sa, const float *__restrict__ logits, const qs_row_param *__re
         }
         const qs_row_param P = stream_param(a, cur.row);
         const int s2 = s0 == 0 ? 2 : s0 - 1;          // (s0 + 2) mod 3
-        part_step(X, a, cur, P, pl.bm[s0], pl.hitw[s0], (idx - run.begin) & 1, pl, [&] {
+        part_step<GF>(X, a, cur, P, pl.bm[s0], pl.hitw[s0], (idx - run.begin) & 1, pl, [&] {
             // slot s0 was read by this part's pass 1 (done): cleared for part idx + 3;
             // slot s2 (cleared a part ago) gets part idx + 2's ids
             bitmap_zero(pl.bm[s0], pl.hitw[s0]);
@@ -1103,14 +1155,15 @@ int qs_part_resident(void) {
     int dev = 0, ncu = 0, nb = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_part, NT, 0) != hipSuccess || nb < 1)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_part<false>, NT, 0) != hipSuccess ||
+        nb < 1)
         return 0;
     return ncu * nb;
 }
 
 int qs_part_launch(const float *logits, int64_t row_stride, int n_rows, int n_vocab,
                    const RowState &st, const Scratch &sc, int32_t *out, qs_pick_diag *diag,
-                   int resident, hipStream_t stream, hipEvent_t mid) {
+                   int resident, hipStream_t stream, hipEvent_t mid, bool all_greedy) {
     PartArgs a;
     a.logits = logits;
     a.stride = row_stride;
@@ -1138,6 +1191,14 @@ int qs_part_launch(const float *logits, int64_t row_stride, int n_rows, int n_vo
     sa.hhead = st.hhead;
     sa.rec = sc.wrec;
     sa.cand = sc.pcand;
+    sa.gbest = sc.gbest;
+    sa.gmaxk = sc.gmaxk;
+    sa.gcnt = sc.gcnt;
+    sa.ring_w = st.ring;
+    sa.hlen_w = st.hlen;
+    sa.hhead_w = st.hhead;
+    sa.out = out;
+    sa.diag = diag;
     // a persistent grid: the resident workgroups (a multiple of 8 for the XCD mapping), or
     // one per part when there are fewer parts
     const int64_t total = (int64_t)n_rows * a.parts;
@@ -1145,11 +1206,17 @@ int qs_part_launch(const float *logits, int64_t row_stride, int n_rows, int n_vo
     if (a.xcd_map) grid = grid / 8 * 8;
     if (grid > total) grid = a.xcd_map ? (total + 7) / 8 * 8 : total;
     if (grid < 1) grid = 1;
-    hipLaunchKernelGGL(k_part, dim3((unsigned)grid), dim3(NT), 0, stream, sa, sa.logits, sa.prm,
-                       sa.ring, sa.hlen, sa.hhead, sa.rec, sa.cand);
+    // every row greedy, with the scratch for it: each row decided by its last part
+    const bool gf = all_greedy && sc.gbest != nullptr;
+    if (gf)
+        hipLaunchKernelGGL(k_part<true>, dim3((unsigned)grid), dim3(NT), 0, stream, sa,
+                           sa.logits, sa.prm, sa.ring, sa.hlen, sa.hhead, sa.rec, sa.cand);
+    else
+        hipLaunchKernelGGL(k_part<false>, dim3((unsigned)grid), dim3(NT), 0, stream, sa,
+                           sa.logits, sa.prm, sa.ring, sa.hlen, sa.hhead, sa.rec, sa.cand);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && mid) e = hipEventRecord(mid, stream);
-    if (e == hipSuccess) {
+    if (e == hipSuccess && !gf) {
         hipLaunchKernelGGL(k_decide, dim3((unsigned)n_rows), dim3(ND), 0, stream, a);
         e = hipGetLastError();
     }

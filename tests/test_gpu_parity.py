@@ -646,6 +646,75 @@ def test_mode_mixed_rows(qa, oracle, mode):
     buf.free()
 
 
+def test_stream_all_greedy_rows_decided_by_last_part(qa, oracle):
+    """A batch whose rows are all greedy takes the streaming kernel alone: each row's last
+    part to finish reads the row's best (key, ~id) and records it (sample.c:118-134).  16
+    rows at the full vocabulary (15 parts each): ties within and across parts, +inf, all
+    -inf, NaNs (one at id 0), a signed-zero max, one finite logit, a maximum in the last
+    part's tail, and rows whose largest logits are penalised history ids; against the CPU
+    restatement over four picks (the per-row counters are reset between picks), then the
+    same rows picked again in a mixed batch (the decision kernel's greedy path)."""
+    rng = np.random.default_rng(33)
+    B, V = 16, 151936
+    x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+    x[1, :] = np.float32(0.25)                     # all equal: id 0
+    x[2, [20000, 90000, 140000]] = np.float32(30.0)  # equal maxima in three parts
+    x[3, 1000] = np.float32(np.inf)
+    x[4, :] = np.float32(-np.inf)                  # all -inf: id 0
+    x[5, ::7] = np.float32(np.nan)
+    x[6, 0] = np.float32(np.nan)                   # NaN at id 0: id 0
+    x[7, :] = -np.abs(x[7, :]) - np.float32(1.0)   # the max is a signed zero
+    x[7, 300] = np.float32(-0.0)
+    x[7, 600] = np.float32(0.0)
+    x[8, :] = np.float32(-np.inf)                  # one finite logit
+    x[8, 123456] = np.float32(-7.0)
+    x[9, V - 2] = np.float32(40.0)                 # in the last part's tail
+    x[10, 5000] = np.float32(12.0)                 # penalised below the runner-up
+    x[10, 6000] = np.float32(10.0)
+    x[11, 7000] = np.float32(-0.5)                 # a negative max, penalised by product
+    x[11, :7000] = np.minimum(x[11, :7000], np.float32(-0.6))
+    x[11, 7001:] = np.minimum(x[11, 7001:], np.float32(-0.6))
+    buf = qa.DeviceBuffer.from_array(x)
+    per_row, hists = [], []
+    for r in range(B):
+        rp = 1.0 if r < 10 else 1.3
+        cfg = (0.0, 0.9, 40, 0.05, rp, 64)
+        h = rng.integers(0, V, 16).astype(np.int32)
+        if r == 10:
+            h[3] = 5000
+        if r == 11:
+            h[5] = 7000
+        per_row.append((cfg, int(rng.integers(1, 2**62))))
+        hists.append(h)
+    b = qa.Batch(B, V, 64)
+    for r, (cfg, seed) in enumerate(per_row):
+        b.config(r, 1, *cfg, seeds=[seed])
+        b.set_history(r, hists[r])
+    assert b.resolve_mode(buf.ptr, V, B, V) == qa.MODE_STREAM
+    outs = [b.pick(buf.ptr, V, B, V, diag=True) for _ in range(4)]
+    sams = []
+    for r in range(B):
+        s = oracle.sampler()
+        s.config(*per_row[r][0], seed=per_row[r][1])
+        s.set_history(hists[r])
+        for k in range(4):
+            want = s.pick(x[r])
+            assert int(outs[k][0][r]) == want, (r, k, want, int(outs[k][0][r]))
+            assert outs[k][1][r].path == qa.PATH_GREEDY, (r, k)
+        rs, h = b.get_state(r)
+        assert rs == s.rng and (h == s.history()).all(), r
+        sams.append(s)
+    # a sampling row joins: the greedy rows go through the decision kernel instead
+    b.config(B - 1, 1, 0.8, 0.95, 40, 0.05, 1.0, 64, seeds=[99])
+    sams[B - 1] = oracle.sampler()
+    sams[B - 1].config(0.8, 0.95, 40, 0.05, 1.0, 64, seed=99)
+    ids = b.pick(buf.ptr, V, B, V)
+    for r in range(B):
+        assert int(ids[r]) == sams[r].pick(x[r]), r
+    b.close()
+    buf.free()
+
+
 @pytest.mark.parametrize("mode", ["auto", "split"])
 def test_history_layouts(qa, oracle, mode):
     """Histories in unusual shapes: runs of consecutive ids (several in one thread's
