@@ -281,6 +281,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
     uint32_t rej_w = 0u;
     int wn = 0, len = 0, first = 1;
     uint32_t th0 = 0u;                              // the ratchet's bound before it is seeded
+    uint32_t thw_r = 0u, stp_r = RATCHET_STEP;      // other rows: this wavefront's statistic
+                                                    // after its first chunk, and its step
     uint32_t wmx_base = 0xFFFFFFFFu;                // the max key the base was last set from
     auto chunk = [&](auto tail_c, float4 (&X)[RU], int j) {
         constexpr bool tail = decltype(tail_c)::value;   // the row's partial last chunk
@@ -486,9 +488,26 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)
             oth = min(oth, dpp_move<0x140, 0xF>(oth));
             const uint32_t othm = (uint32_t)__builtin_amdgcn_readlane((int)oth, 15);
             // (a wavefront's first chunk, before the others have published: its m0-th
-            // largest)
-            const uint32_t thw = halves && !first ? min(h0, h1)
-                                                  : wave_mth(run, wmx, first ? (halves ? 6 : m0) : m);
+            // largest).  Without halves, later chunks raise the first chunk's statistic as a
+            // ratchet (a step up taken when at least m running lane maxima lie strictly
+            // above it, doubled on success and halved on failure): every value it takes
+            // still has m lane maxima at or above it, without a selection every chunk
+            uint32_t thw;
+            if (halves && !first) {
+                thw = min(h0, h1);
+            } else if (first) {
+                thw = wave_mth(run, wmx, halves ? 6 : m0);
+                thw_r = thw;
+            } else {
+                const uint32_t c = thw_r + stp_r > thw_r ? thw_r + stp_r : 0xFFFFFFFFu;
+                if ((int)__popcll(__ballot(run > c)) >= m) {
+                    thw_r = c;
+                    stp_r = stp_r < 0x40000000u ? 2u * stp_r : stp_r;
+                } else {
+                    stp_r = stp_r > 1u ? stp_r >> 1 : 1u;
+                }
+                thw = thw_r;
+            }
             first = 0;
             if (lane == 0) lds_st(&rl.theta[wv], thw);
             th = min(thw, othm);
