@@ -15,6 +15,8 @@
 //      the part's share of the reference's softmax denominator (qs_cert.h);
 //   4. the logits at or above the threshold as (key, id) candidates, stored with the
 //      part's sums.
+// When every row is greedy, k_part alone: each part joins its first argmax into the row's
+// by device-wide atomic maxima, and the row's last part records it (greedy_part_done).
 // k_decide, B workgroups of 256 threads: the row's denominator interval, the candidates'
 // exact numerators (the host-libm-equal expf) and the cuts and draw proved for every
 // normaliser of the interval (cert_row_wave / cert_row_block).  A row the proof does not
@@ -927,8 +929,9 @@ __global__ void __launch_bounds__(ND) k_decide(PartArgs a) {
     RowHist hist{0ull, 0, 0};
     if (tid < 64 && !greedy) hist = row_hist(st, row);
     if (NL <= 128) {
-        // rows of up to 16 parts: wavefront 0 gathers and decides; the workgroup joins only
-        // for the block decision, a greedy row's scan or the exact path
+        // rows of up to 16 parts: greedy rows by wavefront 0 alone, sampling rows by the
+        // workgroup (decide_par); the whole workgroup then takes the block decision, a
+        // greedy row's scan or the exact path
         if (greedy) {
             if (wv == 0) {
                 const int s0 = decide_wave0(a, row, P, dl, hist);
