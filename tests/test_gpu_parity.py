@@ -715,6 +715,49 @@ def test_stream_all_greedy_rows_decided_by_last_part(qa, oracle):
     buf.free()
 
 
+@pytest.mark.parametrize("mode", ["stream", "row", "greedy_stream"])
+def test_random_row_configs(qa, oracle, mode):
+    """24 rows at the full vocabulary with random per-row settings (temperature 0 to 1.5,
+    top-k off to 300, top-p, min-p, penalties over random histories with repeats), logits
+    from three shapes (normal, peaked, heavy-tailed), through the streaming kernel (its
+    workgroup decision of rows of 15 parts), the row kernel, or, with every row greedy, the
+    streaming kernel alone; ids and final states against the CPU restatement over two
+    picks."""
+    rng = np.random.default_rng({"stream": 51, "row": 52, "greedy_stream": 53}[mode])
+    B, V = 24, 151936
+    x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+    for r in range(0, B, 3):
+        x[r, int(rng.integers(0, V))] += np.float32(rng.uniform(5, 15))
+    for r in range(1, B, 3):
+        x[r] = (rng.standard_t(3, V) * 2.0).astype(np.float32)
+    buf = qa.DeviceBuffer.from_array(x)
+    per_row, hists = [], []
+    for r in range(B):
+        t = 0.0 if mode == "greedy_stream" else float(rng.choice([0.0, 0.3, 0.7, 1.0, 1.5]))
+        cfg = (t, float(rng.choice([1.0, 0.95, 0.9, 0.5])),
+               int(rng.choice([0, 1, 5, 40, 64, 100, 300])),
+               float(rng.choice([0.0, 0.02, 0.1])), float(rng.choice([1.0, 1.1, 1.5])),
+               int(rng.choice([0, 32, 64])))
+        per_row.append((cfg, int(rng.integers(1, 2**62))))
+        hists.append(rng.integers(0, 4000, 48).astype(np.int32))
+    b = qa.Batch(B, V, 64)
+    b.set_mode(qa.MODE_ROW if mode == "row" else qa.MODE_STREAM)
+    for r, (cfg, seed) in enumerate(per_row):
+        b.config(r, 1, *cfg, seeds=[seed])
+        b.set_history(r, hists[r])
+    outs = [b.pick(buf.ptr, V, B, V) for _ in range(2)]
+    for r in range(B):
+        s = oracle.sampler()
+        s.config(*per_row[r][0], seed=per_row[r][1])
+        s.set_history(hists[r])
+        for k in range(2):
+            assert int(outs[k][r]) == s.pick(x[r]), (mode, r, k, per_row[r][0])
+        rs, h = b.get_state(r)
+        assert rs == s.rng and (h == s.history()).all(), (mode, r)
+    b.close()
+    buf.free()
+
+
 @pytest.mark.parametrize("mode", ["auto", "split"])
 def test_history_layouts(qa, oracle, mode):
     """Histories in unusual shapes: runs of consecutive ids (several in one thread's
